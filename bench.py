@@ -1,0 +1,154 @@
+"""Benchmark of the GPT-2 token loop on one MI355X.
+
+Default workload (BASELINE.json metric "decode tokens/s (GPT-2 small b=1) +
+achieved HBM GB/s as % of peak"): configuration c1 = GPT-2 small, fp32,
+random-init N(0, 0.02) weights from seed 1234, batch 1, prompt of 32 uniform
+random ids, greedy decode of 64 tokens (1 prefill + 63 decode steps).
+
+One "step" is one such generate_cached job on weights already resident in
+HBM. `value` = decode tokens/s over the timed steps (decode time measured with
+HIP events on the library's stream); prefill is reported separately.
+Prints ONE JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tokens/s (GPT-2 small b=1) + achieved HBM GB/s as % of peak"
+
+WORKLOADS = {
+    # name: (shape, batch, prompt, new tokens, storage)
+    "c1": ("small", 1, 32, 64, "f32"),
+    "c2": ("small", 8, 128, 256, "f32"),
+    "c3": ("medium", 1, 512, 512, "f32"),
+    "c5": ("xl", 16, 64, 256, "bf16"),
+}
+
+
+def decode_bytes(sh, B, past, wbytes):
+    """Algorithmic HBM bytes of one decode step at past length `past`:
+    weights once, KV read for past+1 positions plus the new row written,
+    embedding rows read, logits written."""
+    L, d, V = sh.n_layer, sh.n_embd, sh.vocab_size
+    weights = (L * (12 * d * d + 13 * d) + V * d + 2 * d)
+    # matrices and wte in storage type, LN/bias in f32
+    mats = L * 12 * d * d + V * d
+    wb = mats * wbytes + (weights - mats) * 4
+    kv = B * L * 2 * d * 4 * (past + 2)
+    emb = B * 2 * d * 4
+    return wb + kv + emb + B * V * 4
+
+
+def cpu_baseline(sd, sh, prompt, n_decode):
+    """Time the CPU oracle (a C restatement of gpt2.rs, 1 thread, as the
+    reference's single-threaded ndarray GEMM) on a bounded c1 sample."""
+    from oracle import oracle as O
+    O.build()
+    m = O.OracleModel.from_shape(sd, sh, threads=1)
+    c = m.new_cache()
+    t0 = time.perf_counter()
+    lg = m.forward_cached(prompt, c)
+    t1 = time.perf_counter()
+    tok = O.argmax(lg[-1])
+    for _ in range(n_decode):
+        lg = m.forward_cached([tok], c)
+        tok = O.argmax(lg[0])
+    t2 = time.perf_counter()
+    return {"value": n_decode / (t2 - t1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"c1 prompt {len(prompt)} prefill ({(t1 - t0) * 1e3:.0f} ms) then {n_decode} greedy decode "
+                      f"steps; oracle/gpt2_oracle.c (C restatement of gpt2.rs), 1 thread",
+            "prefill_tok_s": len(prompt) / (t1 - t0)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="c1", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-decode-steps", type=int, default=24)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
+              "sharding is described in DESIGN.md, not run", file=sys.stderr)
+        sys.exit(2)
+
+    from rusttorch_amd import synth
+    from rusttorch_amd.gpt2 import Gpt2Config, Gpt2Model
+
+    shape_name, B, n_prompt, n_new, storage = WORKLOADS[a.workload]
+    sh = synth.SHAPES[shape_name]
+    t = time.perf_counter()
+    sd = synth.make_weights(sh, bf16=(storage == "bf16"))
+    print(f"[bench] weights generated in {time.perf_counter() - t:.1f}s", file=sys.stderr, flush=True)
+    cfg = Gpt2Config(sh.vocab_size, sh.n_positions, sh.n_embd, sh.n_layer, sh.n_head, sh.layer_norm_epsilon)
+    m = Gpt2Model.from_state_dict(sd, cfg, storage=storage)
+    prompts = np.stack([synth.make_tokens(n_prompt, sh.vocab_size, stream=b) for b in range(B)])
+    print("[bench] model resident; warming up", file=sys.stderr, flush=True)
+    for _ in range(a.warmup):
+        m.generate_cached_batched(prompts, n_new)
+    t0 = time.perf_counter()
+    tims = []
+    ids = None
+    for _ in range(a.steps):
+        ids, tm = m.generate_cached_batched(prompts, n_new, timing=True)
+        tims.append(tm)
+    wall = time.perf_counter() - t0
+    print("[bench] timed steps done", file=sys.stderr, flush=True)
+
+    dec_ms = sum(t["decode_ms"] for t in tims)
+    pre_ms = sum(t["prefill_ms"] for t in tims)
+    dec_steps = sum(t["decode_steps"] for t in tims)
+    dec_tok_s = B * dec_steps / (dec_ms / 1e3)
+    wbytes = 2 if storage == "bf16" else 4
+    step_bytes = [decode_bytes(sh, B, n_prompt + i, wbytes) for i in range(n_new - 1)]
+    avg_bytes = float(np.mean(step_bytes))
+    step_ms = dec_ms / dec_steps
+    kern_ms = sum(t["decode_step_kernel_ms"] for t in tims)
+    kern_n = sum(t["decode_step_kernel_launches"] for t in tims)
+    if kern_n:
+        kernel = "rtg_decode_step (persistent, one launch per decode step)"
+        dur_ms = kern_ms / kern_n
+    else:
+        kernel = "decode step (graph of per-op kernels)"
+        dur_ms = step_ms
+    achieved = avg_bytes / (dur_ms / 1e3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(dec_tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(wall / a.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if storage == "f32" else "f32 (bf16 weights)",
+        "data": "synthetic: seeded N(0,0.02) random-init weights, uniform random token ids",
+        "config": {"workload": f"{a.workload}: GPT-2 {shape_name}, batch {B}, prompt {n_prompt}, greedy {n_new}",
+                   "batch": B, "prompt": n_prompt, "new_tokens": n_new, "weights": storage},
+        "prefill_tok_s": round(B * n_prompt * a.steps / (pre_ms / 1e3), 1),
+        "decode_ms_per_token_step": round(step_ms, 4),
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "bytes_per_launch": int(avg_bytes), "avg_launch_ms": round(dur_ms, 5), "traffic": None},
+        "first_ids": ids[0, n_prompt:n_prompt + 8].tolist(),
+    }
+    if not a.no_cpu and a.workload == "c1":
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(sd, sh, prompts[0], a.cpu_decode_steps)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

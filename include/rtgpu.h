@@ -1,0 +1,153 @@
+/* rtgpu: MI355X (gfx950) GPT-2 token loop behind a C ABI.
+ *
+ * Each entry point mirrors one item of rusttorch's public GPT-2 API
+ * (rusttorch-core/src/nn/gpt2.rs, re-exported at nn/mod.rs:50,94) and follows
+ * the conventions of rusttorch's own C ABI (rusttorch-core/src/ffi/):
+ * fallible calls return rtg_result {success, error_msg} like CResult
+ * (ffi/tensor.rs:37-64); the message is owned by the library and released
+ * with rtg_free_error_message (ffi/tensor.rs:66-72); host buffers are
+ * caller-allocated and results are written into them (ffi/ops.rs:26-39).
+ * Error strings are the reference's own (gpt2.rs:224-228, 269-279, 364-374,
+ * 616-618).
+ *
+ * Threading: a model is immutable after construction and may be shared by
+ * threads (gpt2.rs:358 takes &self); a cache binds one HIP stream and must not
+ * be used from two threads at once (gpt2.rs:361 takes &mut KVCache). All calls
+ * are synchronous from the host's point of view, as in the reference.
+ *
+ * There is no CPU fallback: creating a model without a usable gfx950 device
+ * fails with an error. */
+#ifndef RTGPU_H
+#define RTGPU_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* CResult, ffi/tensor.rs:37-64. */
+typedef struct {
+  bool success;
+  char* error_msg; /* NULL on success; free with rtg_free_error_message */
+} rtg_result;
+
+/* Gpt2Config, gpt2.rs:82-104. */
+typedef struct {
+  size_t vocab_size;
+  size_t n_positions;
+  size_t n_embd;
+  size_t n_layer;
+  size_t n_head;
+  float layer_norm_epsilon;
+} rtg_config;
+
+/* GenerationConfig, gpt2.rs:31-79, plus the seed of the sampler (the
+ * reference draws from rand::thread_rng, gpt2.rs:978,1005, so its sampled ids
+ * are not reproducible; greedy decoding ignores the seed). */
+typedef struct {
+  size_t max_new_tokens;
+  float temperature;
+  size_t top_k;
+  float top_p;
+  float repetition_penalty;
+  uint64_t seed;
+} rtg_gen_config;
+
+/* Element type of a host tensor handed to rtg_model_from_host; decoded to
+ * f32 as safetensors.rs:232-348 does (BF16 = bits << 16, :389-391). */
+typedef enum { RTG_F32 = 0, RTG_BF16 = 1, RTG_F16 = 2, RTG_F64 = 3 } rtg_dtype;
+
+/* How the weights are held in HBM. RTG_STORE_BF16 keeps GEMM/GEMV weights as
+ * bfloat16 (round-to-nearest-even) and upcasts them in-kernel; the oracle is
+ * fed the same rounded values. */
+typedef enum { RTG_STORE_F32 = 0, RTG_STORE_BF16 = 1 } rtg_storage;
+
+/* One StateDict entry (nn/state_dict.rs:35-56): name, dtype, shape, data. */
+typedef struct {
+  const char* name;
+  const void* data;
+  rtg_dtype dtype;
+  size_t ndim;
+  const size_t* shape;
+} rtg_named_tensor;
+
+typedef struct rtg_model rtg_model;
+typedef struct rtg_cache rtg_cache;
+
+/* Device-event timings of the last generate call made with this struct. */
+typedef struct {
+  double prefill_ms;     /* forward_cached over the prompt + first argmax */
+  double decode_ms;      /* the (max_new - 1) single-token steps */
+  size_t decode_steps;
+  double decode_step_kernel_ms; /* summed duration of the dominant decode kernel */
+  size_t decode_step_kernel_launches;
+} rtg_timing;
+
+/* rusttorch_init / rusttorch_cleanup / rusttorch_version, ffi/mod.rs:24-48. */
+void rtg_init(void);
+void rtg_cleanup(void);
+const char* rtg_version(void);
+/* rusttorch_free_error_message, ffi/tensor.rs:66-72. */
+void rtg_free_error_message(char* msg);
+
+/* Gpt2Model::from_safetensors, gpt2.rs:214-220 (F32/F64/F16/BF16 tensors).
+ * Error: "Failed to load safetensors: ..." or "Missing weight: <name>". */
+rtg_result rtg_model_from_safetensors(const char* path, const rtg_config* cfg, rtg_storage storage,
+                                      rtg_model** out);
+/* Gpt2Model::from_state_dict, gpt2.rs:223-263. Tensors use the reference's
+ * Conv1D layout [in, out]; the data is copied (uploaded) before returning. */
+rtg_result rtg_model_from_host(const rtg_config* cfg, const rtg_named_tensor* tensors, size_t n,
+                               rtg_storage storage, rtg_model** out);
+void rtg_model_destroy(rtg_model* model);
+/* Gpt2Model::num_parameters, gpt2.rs:541-563. */
+size_t rtg_num_parameters(const rtg_model* model);
+
+/* Gpt2Model::new_cache / KVCache::new, gpt2.rs:349-352, 125-134. The cache
+ * holds `batch` sequences and preallocates n_layer*batch*2*n_head*n_positions*
+ * head_dim f32 in HBM. batch = 1 is the reference's cache. */
+rtg_result rtg_cache_new(const rtg_model* model, size_t batch, rtg_cache** out);
+/* KVCache::len / is_empty / clear, gpt2.rs:137-161. */
+size_t rtg_cache_len(const rtg_cache* cache);
+bool rtg_cache_is_empty(const rtg_cache* cache);
+void rtg_cache_clear(rtg_cache* cache);
+void rtg_cache_destroy(rtg_cache* cache);
+/* Copies cached keys (values != 0: values) of one layer/head/sequence for
+ * positions [0, len) to out[len * head_dim]; a test hook with no reference
+ * counterpart (the reference's LayerKVCache fields are private). */
+rtg_result rtg_cache_read(const rtg_cache* cache, size_t layer, size_t head, size_t seq, int values, float* out);
+
+/* Gpt2Model::forward, gpt2.rs:269-304: logits_out[n * vocab_size]. */
+rtg_result rtg_forward(const rtg_model* model, const uint32_t* ids, size_t n, float* logits_out);
+/* Gpt2Model::forward_cached, gpt2.rs:358-399: logits_out[n * vocab_size]
+ * (may be NULL to skip the device-to-host copy). The cache must have batch 1. */
+rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
+                              float* logits_out);
+/* Gpt2Model::generate (uncached, sliding window), gpt2.rs:311-346.
+ * out receives n + max_new ids. */
+rtg_result rtg_generate(const rtg_model* model, const uint32_t* prompt, size_t n, size_t max_new,
+                        float temperature, uint64_t seed, uint32_t* out);
+/* Gpt2Model::generate_cached, gpt2.rs:405-441. out receives n + max(1, max_new)
+ * ids: like the reference, the prefill token is appended even if max_new == 0. */
+rtg_result rtg_generate_cached(const rtg_model* model, const uint32_t* prompt, size_t n, size_t max_new,
+                               float temperature, uint64_t seed, uint32_t* out);
+/* Gpt2Model::generate_with_config, gpt2.rs:447-474 (+ sample_logits :871-906).
+ * out receives n + max(1, cfg->max_new_tokens) ids. */
+rtg_result rtg_generate_with_config(const rtg_model* model, const uint32_t* prompt, size_t n,
+                                    const rtg_gen_config* cfg, uint32_t* out);
+
+/* Batched extension (new API: the reference is batch-1 only; its oracle for
+ * batch B is B independent calls). ids/prompts are [batch][n] row-major. */
+rtg_result rtg_forward_cached_batched(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
+                                      float* logits_out /* [batch][n][V] or NULL */);
+/* Greedy generate_cached over `batch` equal-length prompts; out is
+ * [batch][n + max(1, max_new)]. timing may be NULL. */
+rtg_result rtg_generate_cached_batched(const rtg_model* model, const uint32_t* prompts, size_t batch, size_t n,
+                                       size_t max_new, uint32_t* out, rtg_timing* timing);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RTGPU_H */

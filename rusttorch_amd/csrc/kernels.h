@@ -1,0 +1,77 @@
+// Launchers for the gfx950 kernels of the GPT-2 token loop.
+//
+// Device layouts (all row-major, all in HBM):
+//   weights W^T [N][K]  : every Conv1D weight of the reference ([in=K][out=N],
+//                         gpt2.rs:15-17) is stored transposed, so each output
+//                         is a dot product over a contiguous K row.
+//   wte [V][d]          : token table; also the tied LM head's W^T.
+//   KV cache            : [layer][seq][head][n_positions][64] f32.
+//   activations         : [rows][cols] f32, rows = seq * T + t.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rtg {
+
+enum WType { W_F32 = 0, W_BF16 = 1 };
+
+// GEMV / GEMM epilogues.
+enum Epi {
+  EPI_BIAS = 0,       // y = acc + bias
+  EPI_BIAS_GELU = 1,  // y = gelu_new(acc + bias)
+  EPI_BIAS_RESID = 2, // y = y + (acc + bias)          (in-place residual)
+  EPI_NONE = 3,       // y = acc                        (LM head)
+};
+
+struct KvDst {
+  float* k;        // cache keys base for this layer: [seq][head][P][64]
+  float* v;
+  int n_head;
+  int n_pos;       // P
+  int d;           // n_embd
+};
+
+// Token + position embedding. ids[rows]; position of row r = pos0 + (r % T),
+// or, when pos_dev != nullptr, *pos_dev (decode: T == 1).
+void launch_embed(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* ids, int rows, int T,
+                  int pos0, const int* pos_dev, int d, float* x);
+
+// Row LayerNorm (gpt2.rs:636-666), rows x d.
+void launch_layernorm(hipStream_t s, const float* x, const float* w, const float* b, float eps, int rows, int d,
+                      float* out);
+
+// Decode GEMV: y[b][n] = epi(sum_k x[b][k] * W[n][k]) for b < B (B <= 16).
+void launch_gemv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
+                 float* y, int ldy, int N, int K, int epi);
+// Decode QKV GEMV: q part to q[b][d]; k/v parts into the cache at *pos_dev.
+void launch_gemv_qkv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
+                     float* q, int ldq, int d, KvDst kv, const int* pos_dev);
+
+// Decode attention over the cache for positions [0, *pos_dev] (gpt2.rs:772-834).
+void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc,
+                        int n_head, int n_pos, const int* pos_dev, float* out, int ldo);
+
+// Greedy argmax over rows of logits (gpt2.rs:858-868) into packed keys.
+void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V, unsigned long long* keys);
+// Decode bookkeeping: token[b] = unpack(keys[b]); ids_out[b*ld + *step_dev] = token;
+// keys reset; *pos_dev += 1; *step_dev += 1.
+void launch_finalize(hipStream_t s, int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
+                     int* pos_dev, int* step_dev);
+// Extract tokens from keys without touching counters (prefill).
+void launch_keys_to_tokens(hipStream_t s, int B, unsigned long long* keys, uint32_t* token);
+void launch_reset_keys(hipStream_t s, int B, unsigned long long* keys);
+
+// Prefill GEMM on MFMA: C[M][N] = epi(A[M][K] * W[N][K]^T); C row stride ldc.
+void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
+                 long ldc, int M, int N, int K, int epi);
+// Prefill: append k/v columns of qkv [S*T][3d] into the cache at past.. past+T.
+void launch_kv_append(hipStream_t s, const float* qkv, int S, int T, int past, KvDst kv);
+// Prefill causal attention for S sequences of T new tokens at offset past.
+void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past, const float* kc, const float* vc,
+                         int n_head, int n_pos, int d, float* out);
+
+// bf16 conversion / transposition used once at model load.
+void launch_transpose_to(hipStream_t s, const float* src, int rows, int cols, void* dst, int wtype);
+void launch_convert_to(hipStream_t s, const float* src, long n, void* dst, int wtype);
+
+}  // namespace rtg

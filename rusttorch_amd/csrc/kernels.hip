@@ -1,0 +1,709 @@
+// gfx950 kernels for the GPT-2 token loop: embedding, LayerNorm, decode GEMV
+// with fused epilogues, attention over the KV cache (decode and causal
+// prefill), argmax, and an fp32 MFMA GEMM for prefill.
+//
+// Each kernel states the reference function it computes (file:line in
+// rusttorch-core/src/nn/gpt2.rs). Arithmetic is fp32 throughout; weights may
+// be stored as bf16 and widened with the reference's bf16_to_f32 (bits << 16,
+// nn/safetensors.rs:389-391).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+namespace rtg {
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Block reduction over blockDim.x threads (multiple of 64, <= 1024). red has
+// >= 16 floats of LDS. Returns the total to every thread.
+template <bool MAX>
+__device__ __forceinline__ float block_reduce(float v, float* red) {
+  v = MAX ? wave_max(v) : wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = red[0];
+  for (int w = 1; w < nw; ++w) t = MAX ? fmaxf(t, red[w]) : t + red[w];
+  return t;
+}
+
+// gelu_new, gpt2.rs:837-847, with the reference's association.
+__device__ __forceinline__ float gelu_new(float x) {
+  const float sqrt_2_pi = 0.7978845608028654f;  // (2.0f32 / PI).sqrt() rounded to f32
+  float inner = sqrt_2_pi * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// Load E consecutive weights (16 bytes) widened to f32.
+template <int WT>
+struct WVec;
+template <>
+struct WVec<W_F32> {
+  static constexpr int E = 4;
+  __device__ __forceinline__ static void load(const void* base, size_t idx, float* out) {
+    float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + idx);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  }
+};
+template <>
+struct WVec<W_BF16> {
+  static constexpr int E = 8;
+  __device__ __forceinline__ static void load(const void* base, size_t idx, float* out) {
+    uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + idx);
+    out[0] = __uint_as_float(v.x << 16); out[1] = __uint_as_float(v.x & 0xffff0000u);
+    out[2] = __uint_as_float(v.y << 16); out[3] = __uint_as_float(v.y & 0xffff0000u);
+    out[4] = __uint_as_float(v.z << 16); out[5] = __uint_as_float(v.z & 0xffff0000u);
+    out[6] = __uint_as_float(v.w << 16); out[7] = __uint_as_float(v.w & 0xffff0000u);
+  }
+};
+
+__device__ __forceinline__ float load_w1(const void* base, size_t idx, int wtype) {
+  if (wtype == W_F32) return reinterpret_cast<const float*>(base)[idx];
+  return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[idx]);
+}
+
+// ---------------------------------------------------------------------------
+// embedding (gpt2.rs:377-384: embedding_lookup(wte) + embedding_lookup(wpe) + add)
+// ---------------------------------------------------------------------------
+
+__global__ void embed_kernel(const void* __restrict__ wte, int wtype, const float* __restrict__ wpe,
+                             const uint32_t* __restrict__ ids, int T, int pos0, const int* __restrict__ pos_dev,
+                             int d, float* __restrict__ x) {
+  const int r = blockIdx.x;
+  const int pos = pos_dev ? *pos_dev : pos0 + (r % T);
+  const size_t tok = ids[r];
+  for (int j = threadIdx.x; j < d; j += blockDim.x)
+    x[(size_t)r * d + j] = load_w1(wte, tok * d + j, wtype) + wpe[(size_t)pos * d + j];
+}
+
+void launch_embed(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* ids, int rows, int T,
+                  int pos0, const int* pos_dev, int d, float* x) {
+  embed_kernel<<<rows, 256, 0, s>>>(wte, wtype, wpe, ids, T, pos0, pos_dev, d, x);
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm (gpt2.rs:636-666): two-pass mean / variance, one block per row.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                        const float* __restrict__ b, float eps, int d,
+                                                        float* __restrict__ out) {
+  __shared__ float red[16];
+  const float* row = x + (size_t)blockIdx.x * d;
+  float s = 0.f;
+  for (int j = threadIdx.x; j < d; j += blockDim.x) s += row[j];
+  const float mean = block_reduce<false>(s, red) / (float)d;
+  float v = 0.f;
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    float t = row[j] - mean;
+    v += t * t;
+  }
+  const float var = block_reduce<false>(v, red) / (float)d;
+  const float inv_std = 1.0f / sqrtf(var + eps);
+  for (int j = threadIdx.x; j < d; j += blockDim.x)
+    out[(size_t)blockIdx.x * d + j] = (row[j] - mean) * inv_std * w[j] + b[j];
+}
+
+void launch_layernorm(hipStream_t s, const float* x, const float* w, const float* b, float eps, int rows, int d,
+                      float* out) {
+  layernorm_kernel<<<rows, 256, 0, s>>>(x, w, b, eps, d, out);
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV: one wave computes R output rows for up to BM sequences. Rows of
+// W^T are contiguous, so each lane streams 16-byte vectors of a row
+// (coalesced 1 KiB per wave instruction) and the wave reduces at the end.
+// conv1d_forward, gpt2.rs:628-633 (matmul + add_broadcast), with the
+// epilogues of forward_layer_cached (gpt2.rs:493-537).
+// ---------------------------------------------------------------------------
+
+struct GemvOut {
+  float* y;
+  int ldy;
+  int epi;
+  // QKV mode (q != nullptr): columns [0,d) -> q, [d,2d) -> K cache, [2d,3d) -> V cache.
+  float* q;
+  int ldq;
+  int d;
+  KvDst kv;
+  const int* pos_dev;
+};
+
+template <int BM, int WT, int R>
+__global__ __launch_bounds__(256) void gemv_kernel(const void* __restrict__ W, const float* __restrict__ bias,
+                                                   const float* __restrict__ x, int ldx, int nb, int N, int K,
+                                                   GemvOut o) {
+  constexpr int E = WVec<WT>::E;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= N) return;
+  float acc[R][BM];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < BM; ++b) acc[r][b] = 0.f;
+
+  for (int k = lane * E; k < K; k += 64 * E) {
+    float xv[BM][E];
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      if (b < nb) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+          float4 t = *reinterpret_cast<const float4*>(x + (size_t)b * ldx + k + e);
+          xv[b][e] = t.x; xv[b][e + 1] = t.y; xv[b][e + 2] = t.z; xv[b][e + 3] = t.w;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) xv[b][e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (row0 + r < N) {
+        float wv[E];
+        WVec<WT>::load(W, (size_t)(row0 + r) * K + k, wv);
+#pragma unroll
+        for (int b = 0; b < BM; ++b)
+#pragma unroll
+          for (int e = 0; e < E; ++e) acc[r][b] = fmaf(wv[e], xv[b][e], acc[r][b]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < BM; ++b) acc[r][b] = wave_sum(acc[r][b]);
+
+  // Lane (r * BM + b) writes output (row0 + r, b); R * BM <= 64.
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      const int n = row0 + r;
+      if (lane == r * BM + b && n < N && b < nb) {
+        float v = acc[r][b];
+        if (o.q) {
+          v = v + bias[n];
+          const int d = o.d;
+          if (n < d) {
+            o.q[(size_t)b * o.ldq + n] = v;
+          } else {
+            const int c = n - (n < 2 * d ? d : 2 * d);
+            const int hd = d / o.kv.n_head;
+            const int h = c / hd, dd = c - h * hd;
+            float* base = n < 2 * d ? o.kv.k : o.kv.v;
+            const size_t off = (((size_t)b * o.kv.n_head + h) * o.kv.n_pos + *o.pos_dev) * hd + dd;
+            base[off] = v;
+          }
+        } else {
+          float* yp = o.y + (size_t)b * o.ldy + n;
+          if (o.epi == EPI_BIAS) *yp = v + bias[n];
+          else if (o.epi == EPI_BIAS_GELU) *yp = gelu_new(v + bias[n]);
+          else if (o.epi == EPI_BIAS_RESID) *yp = *yp + (v + bias[n]);
+          else *yp = v;
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int WT>
+static void gemv_dispatch_r(hipStream_t s, const void* W, const float* bias, const float* x, int ldx, int nb, int N,
+                            int K, const GemvOut& o) {
+  // Four rows per wave once there are plenty of rows (LM head), else one.
+  if (N >= 16384 && BM <= 8) {
+    constexpr int R = 4;
+    const int waves = (N + R - 1) / R;
+    gemv_kernel<BM, WT, R><<<(waves + 3) / 4, 256, 0, s>>>(W, bias, x, ldx, nb, N, K, o);
+  } else {
+    const int waves = N;
+    gemv_kernel<BM, WT, 1><<<(waves + 3) / 4, 256, 0, s>>>(W, bias, x, ldx, nb, N, K, o);
+  }
+}
+
+template <int WT>
+static void gemv_dispatch_b(hipStream_t s, int nb, const void* W, const float* bias, const float* x, int ldx, int N,
+                            int K, const GemvOut& o) {
+  if (nb <= 1) gemv_dispatch_r<1, WT>(s, W, bias, x, ldx, nb, N, K, o);
+  else if (nb <= 2) gemv_dispatch_r<2, WT>(s, W, bias, x, ldx, nb, N, K, o);
+  else if (nb <= 4) gemv_dispatch_r<4, WT>(s, W, bias, x, ldx, nb, N, K, o);
+  else if (nb <= 8) gemv_dispatch_r<8, WT>(s, W, bias, x, ldx, nb, N, K, o);
+  else gemv_dispatch_r<16, WT>(s, W, bias, x, ldx, nb, N, K, o);
+}
+
+void launch_gemv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
+                 float* y, int ldy, int N, int K, int epi) {
+  GemvOut o{};
+  o.y = y; o.ldy = ldy; o.epi = epi;
+  if (wtype == W_F32) gemv_dispatch_b<W_F32>(s, B, W, bias, x, ldx, N, K, o);
+  else gemv_dispatch_b<W_BF16>(s, B, W, bias, x, ldx, N, K, o);
+}
+
+void launch_gemv_qkv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
+                     float* q, int ldq, int d, KvDst kv, const int* pos_dev) {
+  GemvOut o{};
+  o.q = q; o.ldq = ldq; o.d = d; o.kv = kv; o.pos_dev = pos_dev;
+  if (wtype == W_F32) gemv_dispatch_b<W_F32>(s, B, W, bias, x, ldx, 3 * d, d, o);
+  else gemv_dispatch_b<W_BF16>(s, B, W, bias, x, ldx, 3 * d, d, o);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention, multi_head_attention_cached (gpt2.rs:772-834) for one new
+// token per sequence: one block per (head, sequence). Scores live in LDS; the
+// softmax is max / exp / sum / divide as in the reference, then P @ V.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, int ldq,
+                                                          const float* __restrict__ kc, const float* __restrict__ vc,
+                                                          int H, int P, int hd, const int* __restrict__ pos_dev,
+                                                          float* __restrict__ out, int ldo) {
+  extern __shared__ float sm[];
+  float* qs = sm;          // [hd]
+  float* red = sm + 64;    // [16] block reduction scratch
+  float* pv = sm + 80;     // [4][64]
+  float* sc = sm + 336;    // [P]
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int len = *pos_dev + 1;
+  const size_t head_off = ((size_t)b * H + h) * P * hd;
+  const float* Kh = kc + head_off;
+  const float* Vh = vc + head_off;
+  if (tid < hd) qs[tid] = q[(size_t)b * ldq + h * hd + tid];
+  __syncthreads();
+  const float scale = 1.0f / sqrtf((float)hd);
+  float mx = -INFINITY;
+  for (int j = tid; j < len; j += blockDim.x) {
+    float dot = 0.f;
+    for (int dd = 0; dd < hd; ++dd) dot = fmaf(qs[dd], Kh[(size_t)j * hd + dd], dot);
+    const float sv = dot * scale;
+    sc[j] = sv;
+    mx = fmaxf(mx, sv);
+  }
+  mx = block_reduce<true>(mx, red);
+  float sum = 0.f;
+  for (int j = tid; j < len; j += blockDim.x) {
+    const float e = expf(sc[j] - mx);
+    sc[j] = e;
+    sum += e;
+  }
+  sum = block_reduce<false>(sum, red);
+  for (int j = tid; j < len; j += blockDim.x) sc[j] = sc[j] / sum;
+  __syncthreads();
+  const int dd = tid & 63, part = tid >> 6;
+  float acc = 0.f;
+  if (dd < hd)
+    for (int j = part; j < len; j += 4) acc = fmaf(sc[j], Vh[(size_t)j * hd + dd], acc);
+  pv[part * 64 + dd] = acc;
+  __syncthreads();
+  if (tid < hd) out[(size_t)b * ldo + h * hd + tid] = (pv[tid] + pv[64 + tid]) + (pv[128 + tid] + pv[192 + tid]);
+}
+
+void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc, int n_head,
+                        int n_pos, const int* pos_dev, float* out, int ldo) {
+  // head_dim = ldq-independent: derived by the caller into n_head via ldo.
+  const int hd = ldo / n_head;
+  const size_t smem = (336 + (size_t)n_pos) * sizeof(float);
+  attn_decode_kernel<<<dim3(n_head, B), 256, smem, s>>>(q, ldq, kc, vc, n_head, n_pos, hd, pos_dev, out, ldo);
+}
+
+// ---------------------------------------------------------------------------
+// Argmax (argmax_f32, gpt2.rs:858-868): strict '>' from -inf, first index wins,
+// NaN never wins. Packed key = (orderable(f) << 32) | ~idx, reduced with a
+// 64-bit atomic max; key 0 (nothing > -inf) decodes to index 0.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ unsigned long long pack_key(float v, uint32_t idx) {
+  if (!(v > -INFINITY)) return 0ull;  // -inf and NaN never win
+  uint32_t b = __float_as_uint(v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)b << 32) | (unsigned long long)(~idx);
+}
+
+__device__ __forceinline__ uint32_t unpack_idx(unsigned long long key) {
+  return key == 0ull ? 0u : ~(uint32_t)(key & 0xffffffffull);
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, long ld, int V,
+                                                     unsigned long long* keys) {
+  __shared__ unsigned long long red[4];
+  const int row = blockIdx.y;
+  const float* p = logits + (size_t)row * ld;
+  unsigned long long best = 0ull;
+  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < V; j += gridDim.x * blockDim.x) {
+    unsigned long long k = pack_key(p[j], (uint32_t)j);
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    unsigned long long o = __shfl_xor(best, off, 64);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) best = red[w] > best ? red[w] : best;
+    atomicMax(&keys[row], best);
+  }
+}
+
+void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V, unsigned long long* keys) {
+  int blocks = (V + 4095) / 4096;
+  if (blocks > 64) blocks = 64;
+  argmax_kernel<<<dim3(blocks, rows), 256, 0, s>>>(logits, ld, V, keys);
+}
+
+__global__ void finalize_kernel(int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
+                                int* pos_dev, int* step_dev) {
+  const int b = threadIdx.x;
+  const int step = *step_dev;
+  __syncthreads();
+  if (b < B) {
+    const uint32_t t = unpack_idx(keys[b]);
+    token[b] = t;
+    if (ids_out) ids_out[(size_t)b * ld_ids + step] = t;
+    keys[b] = 0ull;
+  }
+  __syncthreads();
+  if (b == 0) {
+    *pos_dev += 1;
+    *step_dev = step + 1;
+  }
+}
+
+void launch_finalize(hipStream_t s, int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
+                     int* pos_dev, int* step_dev) {
+  finalize_kernel<<<1, 64, 0, s>>>(B, keys, token, ids_out, ld_ids, pos_dev, step_dev);
+}
+
+__global__ void keys_to_tokens_kernel(int B, unsigned long long* keys, uint32_t* token) {
+  const int b = threadIdx.x;
+  if (b < B) {
+    token[b] = unpack_idx(keys[b]);
+    keys[b] = 0ull;
+  }
+}
+
+void launch_keys_to_tokens(hipStream_t s, int B, unsigned long long* keys, uint32_t* token) {
+  keys_to_tokens_kernel<<<1, 64, 0, s>>>(B, keys, token);
+}
+
+__global__ void reset_keys_kernel(int B, unsigned long long* keys) {
+  if ((int)threadIdx.x < B) keys[threadIdx.x] = 0ull;
+}
+
+void launch_reset_keys(hipStream_t s, int B, unsigned long long* keys) { reset_keys_kernel<<<1, 64, 0, s>>>(B, keys); }
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM on fp32 MFMA (v_mfma_f32_32x32x2f32):
+//   C[M][N] = epi(A[M][K] . W[N][K]^T)
+// 128x128 block tile, 4 waves in a 2x2 arrangement, each wave 64x64 = 2x2
+// MFMA tiles; BK = 16 with LDS double buffering. LDS holds A and W tiles
+// k-major ([k][m], [k][n]) so MFMA operand reads are conflict-free.
+// Operand layout of v_mfma_f32_32x32x2f32: lane l supplies A[l%32][l/32] and
+// B[l/32][l%32]; accumulator i of lane l is D[(i/4)*8 + (l/32)*4 + i%4][l%32].
+// ---------------------------------------------------------------------------
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int GBM = 128, GBN = 128, GBK = 16, GPAD = 4;
+
+template <int WT>
+__global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, int lda, const void* __restrict__ W,
+                                                   const float* __restrict__ bias, float* __restrict__ C, long ldc,
+                                                   int M, int N, int K, int epi) {
+  __shared__ float As[2][GBK][GBM + GPAD];
+  __shared__ float Ws[2][GBK][GBN + GPAD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
+
+  // Global->LDS mapping: 128 rows x 16 k = 512 float4; thread t loads rows
+  // (t >> 2) and (t >> 2) + 64 at k offset (t & 3) * 4.
+  const int lr = tid >> 2, lk = (tid & 3) * 4;
+  float4 ra[2], rw[2];
+
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int m = m0 + lr + h * 64, n = n0 + lr + h * 64, k = k0 + lk;
+      float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vw = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (m < M) {
+        if (k + 3 < K) {
+          va = *reinterpret_cast<const float4*>(A + (size_t)m * lda + k);
+        } else {
+          float t[4] = {0.f, 0.f, 0.f, 0.f};
+          for (int e = 0; e < 4; ++e)
+            if (k + e < K) t[e] = A[(size_t)m * lda + k + e];
+          va = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      }
+      if (n < N) {
+        if (k + 3 < K) {
+          if (WT == W_F32) {
+            vw = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + (size_t)n * K + k);
+          } else {
+            uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(W) + (size_t)n * K + k);
+            vw = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                             __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+          }
+        } else {
+          float t[4] = {0.f, 0.f, 0.f, 0.f};
+          for (int e = 0; e < 4; ++e)
+            if (k + e < K) t[e] = load_w1(W, (size_t)n * K + k + e, WT);
+          vw = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      }
+      ra[h] = va;
+      rw[h] = vw;
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = lr + h * 64;
+      As[buf][lk + 0][r] = ra[h].x; As[buf][lk + 1][r] = ra[h].y;
+      As[buf][lk + 2][r] = ra[h].z; As[buf][lk + 3][r] = ra[h].w;
+      Ws[buf][lk + 0][r] = rw[h].x; Ws[buf][lk + 1][r] = rw[h].y;
+      Ws[buf][lk + 2][r] = rw[h].z; Ws[buf][lk + 3][r] = rw[h].w;
+    }
+  };
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int nk = (K + GBK - 1) / GBK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * GBK);
+#pragma unroll
+    for (int kk = 0; kk < GBK; kk += 2) {
+      const int kr = kk + (lane >> 5);
+      float a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = As[cur][kr][wm + i * 32 + (lane & 31)];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = Ws[cur][kr][wn + j * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn + j * 32 + (lane & 31);
+      if (n >= N) continue;
+      const float bv = bias ? bias[n] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (m < M) {
+          float* cp = C + (size_t)m * ldc + n;
+          const float v = acc[i][j][e];
+          if (epi == EPI_BIAS) *cp = v + bv;
+          else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
+          else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
+          else *cp = v;
+        }
+      }
+    }
+  }
+}
+
+void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
+                 long ldc, int M, int N, int K, int epi) {
+  dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
+  if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
+  else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill KV append (LayerKVCache::append with the per-head split of
+// gpt2.rs:500-514): qkv rows [S*T][3d] -> cache positions past .. past+T-1.
+// ---------------------------------------------------------------------------
+
+__global__ void kv_append_kernel(const float* __restrict__ qkv, int T, int past, KvDst kv) {
+  const int r = blockIdx.x;  // s * T + t
+  const int sidx = r / T, t = r - sidx * T;
+  const int d = kv.d, hd = d / kv.n_head;
+  for (int c = threadIdx.x; c < 2 * d; c += blockDim.x) {
+    const int which = c / d, cc = c - which * d;
+    const int h = cc / hd, dd = cc - h * hd;
+    const float v = qkv[(size_t)r * 3 * d + d + c];
+    float* base = which == 0 ? kv.k : kv.v;
+    base[(((size_t)sidx * kv.n_head + h) * kv.n_pos + past + t) * hd + dd] = v;
+  }
+}
+
+void launch_kv_append(hipStream_t s, const float* qkv, int S, int T, int past, KvDst kv) {
+  kv_append_kernel<<<S * T, 256, 0, s>>>(qkv, T, past, kv);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill causal attention (multi_head_attention_cached, gpt2.rs:772-834, for
+// new_len > 1): one thread per query row, keys/values staged through LDS in
+// tiles of 64, exact softmax via the running-max (online) form.
+// ---------------------------------------------------------------------------
+
+constexpr int PQ = 64;   // queries per block (one wave)
+constexpr int PK = 64;   // keys per tile
+constexpr int HDM = 64;  // max head_dim
+
+__global__ __launch_bounds__(64) void attn_prefill_kernel(const float* __restrict__ qkv, int T, int past,
+                                                          const float* __restrict__ kc, const float* __restrict__ vc,
+                                                          int H, int P, int d, int hd, float* __restrict__ out) {
+  __shared__ float Ks[PK][HDM + 1];
+  __shared__ float Vs[PK][HDM + 1];
+  __shared__ float Ss[PQ][PK + 1];
+  const int qb = blockIdx.x, h = blockIdx.y, sidx = blockIdx.z, tid = threadIdx.x;
+  const int i = qb * PQ + tid;
+  const bool active = i < T;
+  const int pabs = past + i;
+  const size_t head_off = ((size_t)sidx * H + h) * P * hd;
+  const float scale = 1.0f / sqrtf((float)hd);
+  float q[HDM], o[HDM];
+#pragma unroll
+  for (int dd = 0; dd < HDM; ++dd) {
+    q[dd] = (active && dd < hd) ? qkv[((size_t)sidx * T + i) * 3 * d + h * hd + dd] : 0.f;
+    o[dd] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const int last_q = min(T, (qb + 1) * PQ) - 1;
+  const int kend = past + last_q;  // inclusive
+  for (int j0 = 0; j0 <= kend; j0 += PK) {
+    __syncthreads();
+    // Stage keys/values j0 .. j0+PK-1 (thread tid loads row j0+tid).
+    {
+      const int j = j0 + tid;
+      for (int dd = 0; dd < HDM; ++dd) {
+        const bool ok = j <= kend && dd < hd;
+        Ks[tid][dd] = ok ? kc[head_off + (size_t)j * hd + dd] : 0.f;
+        Vs[tid][dd] = ok ? vc[head_off + (size_t)j * hd + dd] : 0.f;
+      }
+    }
+    __syncthreads();
+    float tmax = -INFINITY;
+    for (int jj = 0; jj < PK; ++jj) {
+      const int j = j0 + jj;
+      float sv = -INFINITY;
+      if (active && j <= pabs) {
+        float dot = 0.f;
+#pragma unroll
+        for (int dd = 0; dd < HDM; ++dd) dot = fmaf(q[dd], Ks[jj][dd], dot);
+        sv = dot * scale;
+      }
+      Ss[tid][jj] = sv;
+      tmax = fmaxf(tmax, sv);
+    }
+    if (active && tmax > -INFINITY) {
+      const float mn = fmaxf(m, tmax);
+      const float corr = expf(m - mn);
+      l *= corr;
+#pragma unroll
+      for (int dd = 0; dd < HDM; ++dd) o[dd] *= corr;
+      for (int jj = 0; jj < PK; ++jj) {
+        const float sv = Ss[tid][jj];
+        if (sv == -INFINITY) continue;
+        const float p = expf(sv - mn);
+        l += p;
+#pragma unroll
+        for (int dd = 0; dd < HDM; ++dd) o[dd] = fmaf(p, Vs[jj][dd], o[dd]);
+      }
+      m = mn;
+    }
+  }
+  if (active) {
+    const float inv = 1.0f / l;
+    for (int dd = 0; dd < hd; ++dd) out[((size_t)sidx * T + i) * d + h * hd + dd] = o[dd] * inv;
+  }
+}
+
+void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past, const float* kc, const float* vc,
+                         int n_head, int n_pos, int d, float* out) {
+  dim3 grid((T + PQ - 1) / PQ, n_head, S);
+  attn_prefill_kernel<<<grid, PQ, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, d / n_head, out);
+}
+
+// ---------------------------------------------------------------------------
+// Load-time layout conversion: [rows][cols] f32 -> [cols][rows] f32/bf16
+// (Conv1D [in][out] -> W^T [out][in]), and f32 -> bf16 (round to nearest even).
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x40u);
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return (uint16_t)(b >> 16);
+}
+
+__global__ void transpose_kernel(const float* __restrict__ src, int rows, int cols, void* __restrict__ dst,
+                                 int wtype) {
+  __shared__ float tile[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int y = ty; y < 32; y += 8) {
+    const int r = r0 + y, c = c0 + tx;
+    tile[y][tx] = (r < rows && c < cols) ? src[(size_t)r * cols + c] : 0.f;
+  }
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) {
+    const int c = c0 + y, r = r0 + tx;  // dst[c][r]
+    if (c < cols && r < rows) {
+      const float v = tile[tx][y];
+      if (wtype == W_F32) reinterpret_cast<float*>(dst)[(size_t)c * rows + r] = v;
+      else reinterpret_cast<uint16_t*>(dst)[(size_t)c * rows + r] = f32_to_bf16_rne(v);
+    }
+  }
+}
+
+void launch_transpose_to(hipStream_t s, const float* src, int rows, int cols, void* dst, int wtype) {
+  dim3 grid((cols + 31) / 32, (rows + 31) / 32);
+  transpose_kernel<<<grid, 256, 0, s>>>(src, rows, cols, dst, wtype);
+}
+
+__global__ void convert_kernel(const float* __restrict__ src, long n, void* __restrict__ dst, int wtype) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    if (wtype == W_F32) reinterpret_cast<float*>(dst)[i] = src[i];
+    else reinterpret_cast<uint16_t*>(dst)[i] = f32_to_bf16_rne(src[i]);
+  }
+}
+
+void launch_convert_to(hipStream_t s, const float* src, long n, void* dst, int wtype) {
+  long blocks = (n + 255) / 256;
+  if (blocks > 65535) blocks = 65535;
+  if (blocks < 1) blocks = 1;
+  convert_kernel<<<(unsigned)blocks, 256, 0, s>>>(src, n, dst, wtype);
+}
+
+}  // namespace rtg

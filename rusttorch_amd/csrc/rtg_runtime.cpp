@@ -1,0 +1,983 @@
+// Host runtime of the GPT-2 token loop on MI355X, exported through the C ABI
+// in include/rtgpu.h. It owns HBM-resident weights and KV caches and drives
+// the gfx950 kernels of kernels.hip; it never computes model math on the CPU
+// (sampling of non-greedy generation aside, which the reference also does on
+// the host, gpt2.rs:871-1017).
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cmath>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/rtgpu.h"
+#include "decode_persistent.h"
+#include "kernels.h"
+#include "safetensors_reader.h"
+
+using namespace rtg;
+
+namespace {
+
+rtg_result ok() { return rtg_result{true, nullptr}; }
+
+rtg_result err(const std::string& m) {
+  char* s = (char*)malloc(m.size() + 1);
+  memcpy(s, m.c_str(), m.size() + 1);
+  return rtg_result{false, s};
+}
+
+std::string fmt(const char* f, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, f);
+  vsnprintf(buf, sizeof buf, f, ap);
+  va_end(ap);
+  return buf;
+}
+
+struct HipError {
+  std::string msg;
+};
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw HipError{std::string("HIP error in ") + what + ": " + hipGetErrorString(e)};
+}
+#define HIPX(call) hip_check((call), #call)
+
+std::string check_device() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+    return "no HIP device available: rtgpu requires an MI355X (gfx950) GPU";
+  int dev = 0;
+  hipGetDevice(&dev);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return "hipGetDeviceProperties failed";
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return std::string("rtgpu is built for gfx950 (MI355X); found ") + prop.gcnArchName;
+  return "";
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Model
+// ---------------------------------------------------------------------------
+
+struct LayerW {
+  void *wqkv, *waproj, *wfc, *wmproj;  // W^T [N][K] in storage type
+  float *bqkv, *baproj, *bfc, *bmproj;
+  float *ln1w, *ln1b, *ln2w, *ln2b;
+};
+
+struct rtg_model {
+  rtg_config cfg;
+  int hd = 0;
+  int wtype = W_F32;
+  int device = 0;
+  void* arena = nullptr;
+  size_t arena_bytes = 0;
+  void* wte = nullptr;
+  float* wpe = nullptr;
+  float *lnfw = nullptr, *lnfb = nullptr;
+  std::vector<LayerW> layers;
+  size_t nparams = 0;
+  PersistentPlan* pplan = nullptr;
+  // Pool of caches reused by the generate entry points (keyed by batch).
+  std::mutex pool_mu;
+  std::multimap<size_t, rtg_cache*> pool;
+  ~rtg_model();
+};
+
+// ---------------------------------------------------------------------------
+// Cache (+ per-cache stream, work buffers and the captured decode graph)
+// ---------------------------------------------------------------------------
+
+struct rtg_cache {
+  const rtg_model* m = nullptr;
+  size_t batch = 1;
+  size_t len = 0;
+  hipStream_t stream = nullptr;
+  float* k = nullptr;  // [L][B][H][P][hd]
+  float* v = nullptr;
+  size_t layer_stride = 0;  // floats per layer per K (or V)
+  // decode state in device memory
+  int* pos_dev = nullptr;
+  int* step_dev = nullptr;
+  unsigned long long* keys = nullptr;
+  uint32_t* token_dev = nullptr;
+  uint32_t* ids_dev = nullptr;   // [B][P] generated ids
+  uint32_t* ids_in = nullptr;    // [B*P] prompt ids
+  // work buffers, capacity in rows
+  size_t rows_cap = 0;
+  float *x = nullptr, *ln = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
+  size_t logit_rows_cap = 0;
+  float* logits = nullptr;
+  // decode graph over the current buffers
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  PersistentState* pstate = nullptr;
+};
+
+static void free_work(rtg_cache* c) {
+  for (float** p : {&c->x, &c->ln, &c->qkv, &c->att, &c->h}) {
+    if (*p) hipFree(*p);
+    *p = nullptr;
+  }
+  c->rows_cap = 0;
+}
+
+static void destroy_graph(rtg_cache* c) {
+  if (c->graph_exec) hipGraphExecDestroy(c->graph_exec);
+  if (c->graph) hipGraphDestroy(c->graph);
+  c->graph_exec = nullptr;
+  c->graph = nullptr;
+}
+
+static void ensure_rows(rtg_cache* c, size_t rows) {
+  if (rows <= c->rows_cap) return;
+  destroy_graph(c);
+  free_work(c);
+  const size_t d = c->m->cfg.n_embd;
+  size_t cap = std::max<size_t>(rows, 16);
+  HIPX(hipMalloc(&c->x, cap * d * 4));
+  HIPX(hipMalloc(&c->ln, cap * d * 4));
+  HIPX(hipMalloc(&c->qkv, cap * 3 * d * 4));
+  HIPX(hipMalloc(&c->att, cap * d * 4));
+  HIPX(hipMalloc(&c->h, cap * 4 * d * 4));
+  c->rows_cap = cap;
+}
+
+static void ensure_logits(rtg_cache* c, size_t rows) {
+  if (rows <= c->logit_rows_cap) return;
+  destroy_graph(c);
+  if (c->logits) hipFree(c->logits);
+  c->logits = nullptr;
+  size_t cap = std::max<size_t>(rows, 16);
+  HIPX(hipMalloc(&c->logits, cap * c->m->cfg.vocab_size * 4));
+  c->logit_rows_cap = cap;
+}
+
+static rtg_cache* cache_create(const rtg_model* m, size_t batch) {
+  std::unique_ptr<rtg_cache> c(new rtg_cache());
+  c->m = m;
+  c->batch = batch;
+  const size_t L = m->cfg.n_layer, H = m->cfg.n_head, P = m->cfg.n_positions, hd = m->hd;
+  c->layer_stride = batch * H * P * hd;
+  try {
+    HIPX(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    HIPX(hipMalloc(&c->k, std::max<size_t>(L * c->layer_stride, 1) * 4));
+    HIPX(hipMalloc(&c->v, std::max<size_t>(L * c->layer_stride, 1) * 4));
+    HIPX(hipMalloc(&c->pos_dev, 256));
+    HIPX(hipMalloc(&c->step_dev, 256));
+    HIPX(hipMalloc(&c->keys, std::max<size_t>(batch, 1) * 8));
+    HIPX(hipMalloc(&c->token_dev, std::max<size_t>(batch, 1) * 4));
+    HIPX(hipMalloc(&c->ids_dev, std::max<size_t>(batch * P, 1) * 4));
+    HIPX(hipMalloc(&c->ids_in, std::max<size_t>(batch * P, 1) * 4));
+    for (auto& e : c->ev) HIPX(hipEventCreate(&e));
+    HIPX(hipMemsetAsync(c->pos_dev, 0, 256, c->stream));
+    HIPX(hipMemsetAsync(c->step_dev, 0, 256, c->stream));
+    launch_reset_keys(c->stream, (int)batch, c->keys);
+    HIPX(hipStreamSynchronize(c->stream));
+  } catch (const HipError&) {
+    rtg_cache_destroy(c.release());
+    throw;
+  }
+  return c.release();
+}
+
+rtg_model::~rtg_model() {
+  for (auto& kv : pool) rtg_cache_destroy(kv.second);
+  pool.clear();
+  if (pplan) persistent_plan_destroy(pplan);
+  if (arena) hipFree(arena);
+}
+
+// ---------------------------------------------------------------------------
+// Pipelines
+// ---------------------------------------------------------------------------
+
+static KvDst kv_layer(const rtg_cache* c, size_t l) {
+  KvDst kv;
+  kv.k = c->k + l * c->layer_stride;
+  kv.v = c->v + l * c->layer_stride;
+  kv.n_head = (int)c->m->cfg.n_head;
+  kv.n_pos = (int)c->m->cfg.n_positions;
+  kv.d = (int)c->m->cfg.n_embd;
+  return kv;
+}
+
+// forward_cached body for S sequences x T new tokens (gpt2.rs:376-396) on the
+// MFMA prefill path. ids_dev holds S*T ids; logits rows: all S*T (mode 0) or
+// the last row of each sequence (mode 1, written as S rows).
+static void enqueue_prefill(rtg_cache* c, const uint32_t* ids_dev, size_t S, size_t T, size_t past, int logit_mode) {
+  const rtg_model* m = c->m;
+  const int d = (int)m->cfg.n_embd, V = (int)m->cfg.vocab_size, M = (int)(S * T);
+  const float eps = m->cfg.layer_norm_epsilon;
+  hipStream_t s = c->stream;
+  launch_embed(s, m->wte, m->wtype, m->wpe, ids_dev, M, (int)T, (int)past, nullptr, d, c->x);
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const LayerW& L = m->layers[l];
+    KvDst kv = kv_layer(c, l);
+    launch_layernorm(s, c->x, L.ln1w, L.ln1b, eps, M, d, c->ln);
+    launch_gemm(s, c->ln, d, L.wqkv, m->wtype, L.bqkv, c->qkv, 3 * d, M, 3 * d, d, EPI_BIAS);
+    launch_kv_append(s, c->qkv, (int)S, (int)T, (int)past, kv);
+    launch_attn_prefill(s, c->qkv, (int)S, (int)T, (int)past, kv.k, kv.v, kv.n_head, kv.n_pos, d, c->att);
+    launch_gemm(s, c->att, d, L.waproj, m->wtype, L.baproj, c->x, d, M, d, d, EPI_BIAS_RESID);
+    launch_layernorm(s, c->x, L.ln2w, L.ln2b, eps, M, d, c->ln);
+    launch_gemm(s, c->ln, d, L.wfc, m->wtype, L.bfc, c->h, 4 * d, M, 4 * d, d, EPI_BIAS_GELU);
+    launch_gemm(s, c->h, 4 * d, L.wmproj, m->wtype, L.bmproj, c->x, d, M, d, 4 * d, EPI_BIAS_RESID);
+  }
+  launch_layernorm(s, c->x, m->lnfw, m->lnfb, eps, M, d, c->ln);
+  if (logit_mode == 0) {
+    launch_gemm(s, c->ln, d, m->wte, m->wtype, nullptr, c->logits, V, M, V, d, EPI_NONE);
+  } else {
+    // Last row of each sequence: rows (s*T + T-1), stride T*d.
+    launch_gemm(s, c->ln + (T - 1) * d, (int)(T * d), m->wte, m->wtype, nullptr, c->logits, V, (int)S, V, d,
+                EPI_NONE);
+  }
+}
+
+// One decode step for all B sequences of the cache, reading the token from
+// token_dev and the position from pos_dev (both device-resident), writing the
+// argmax token back to token_dev and ids_dev[b][step]. Capturable.
+static void enqueue_decode_step(rtg_cache* c) {
+  const rtg_model* m = c->m;
+  const int d = (int)m->cfg.n_embd, V = (int)m->cfg.vocab_size, B = (int)c->batch;
+  const float eps = m->cfg.layer_norm_epsilon;
+  hipStream_t s = c->stream;
+  const int P = (int)m->cfg.n_positions;
+  if (c->pstate) {
+    persistent_decode_step(c->pstate, s);
+  } else {
+    launch_embed(s, m->wte, m->wtype, m->wpe, c->token_dev, B, 1, 0, c->pos_dev, d, c->x);
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+      const LayerW& L = m->layers[l];
+      KvDst kv = kv_layer(c, l);
+      launch_layernorm(s, c->x, L.ln1w, L.ln1b, eps, B, d, c->ln);
+      launch_gemv_qkv(s, B, L.wqkv, m->wtype, L.bqkv, c->ln, d, c->qkv, d, d, kv, c->pos_dev);
+      launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d);
+      launch_gemv(s, B, L.waproj, m->wtype, L.baproj, c->att, d, c->x, d, d, d, EPI_BIAS_RESID);
+      launch_layernorm(s, c->x, L.ln2w, L.ln2b, eps, B, d, c->ln);
+      launch_gemv(s, B, L.wfc, m->wtype, L.bfc, c->ln, d, c->h, 4 * d, 4 * d, d, EPI_BIAS_GELU);
+      launch_gemv(s, B, L.wmproj, m->wtype, L.bmproj, c->h, 4 * d, c->x, d, d, 4 * d, EPI_BIAS_RESID);
+    }
+    launch_layernorm(s, c->x, m->lnfw, m->lnfb, eps, B, d, c->ln);
+    launch_gemv(s, B, m->wte, m->wtype, nullptr, c->ln, d, c->logits, V, V, d, EPI_NONE);
+    launch_argmax(s, c->logits, V, B, V, c->keys);
+  }
+  launch_finalize(s, B, c->keys, c->token_dev, c->ids_dev, P, c->pos_dev, c->step_dev);
+}
+
+static void set_counters(rtg_cache* c, int pos, int step) {
+  int hv[2] = {pos, step};
+  HIPX(hipMemcpyAsync(c->pos_dev, &hv[0], 4, hipMemcpyHostToDevice, c->stream));
+  HIPX(hipMemcpyAsync(c->step_dev, &hv[1], 4, hipMemcpyHostToDevice, c->stream));
+}
+
+static void ensure_graph(rtg_cache* c) {
+  if (c->graph_exec) return;
+  HIPX(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  enqueue_decode_step(c);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  HIPX(e);
+  c->graph = g;
+  HIPX(hipGraphInstantiate(&c->graph_exec, c->graph, nullptr, nullptr, 0));
+}
+
+// ---------------------------------------------------------------------------
+// Validation shared by the entry points (gpt2.rs:364-377, 616-618)
+// ---------------------------------------------------------------------------
+
+static std::string check_ids(const rtg_model* m, const uint32_t* ids, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    if (ids[i] >= m->cfg.vocab_size)
+      return fmt("Token ID %zu out of range (vocab_size=%zu)", (size_t)ids[i], m->cfg.vocab_size);
+  return "";
+}
+
+static std::string check_cached(const rtg_model* m, size_t past, const uint32_t* ids, size_t n) {
+  if (n == 0) return "Empty input";
+  const size_t total = past + n;
+  if (total > m->cfg.n_positions)
+    return fmt("Total sequence length %zu exceeds max position %zu", total, m->cfg.n_positions);
+  return check_ids(m, ids, n);
+}
+
+// forward_cached for all sequences of a cache: ids [B][n].
+static void forward_cached_impl(rtg_cache* c, const uint32_t* ids, size_t n, float* logits_out) {
+  const rtg_model* m = c->m;
+  const size_t B = c->batch, V = m->cfg.vocab_size;
+  ensure_rows(c, B * n);
+  ensure_logits(c, B * n);
+  HIPX(hipMemcpyAsync(c->ids_in, ids, B * n * 4, hipMemcpyHostToDevice, c->stream));
+  enqueue_prefill(c, c->ids_in, B, n, c->len, 0);
+  if (logits_out) HIPX(hipMemcpyAsync(logits_out, c->logits, B * n * V * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPX(hipStreamSynchronize(c->stream));
+  c->len += n;
+}
+
+static rtg_cache* pool_take(const rtg_model* mc, size_t batch) {
+  rtg_model* m = const_cast<rtg_model*>(mc);
+  {
+    std::lock_guard<std::mutex> g(m->pool_mu);
+    auto it = m->pool.find(batch);
+    if (it != m->pool.end()) {
+      rtg_cache* c = it->second;
+      m->pool.erase(it);
+      c->len = 0;
+      return c;
+    }
+  }
+  return cache_create(mc, batch);
+}
+
+static void pool_give(const rtg_model* mc, rtg_cache* c) {
+  rtg_model* m = const_cast<rtg_model*>(mc);
+  std::lock_guard<std::mutex> g(m->pool_mu);
+  m->pool.emplace(c->batch, c);
+}
+
+struct PoolLease {
+  const rtg_model* m;
+  rtg_cache* c;
+  PoolLease(const rtg_model* mm, size_t b) : m(mm), c(pool_take(mm, b)) {}
+  ~PoolLease() {
+    if (c) pool_give(m, c);
+  }
+};
+
+// Greedy generate_cached over B equal-length prompts (gpt2.rs:405-441).
+static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t B, size_t n, size_t max_new,
+                            uint32_t* out, rtg_timing* timing) {
+  PoolLease lease(m, B);
+  rtg_cache* c = lease.c;
+  const size_t V = m->cfg.vocab_size, P = m->cfg.n_positions;
+  const size_t steps = max_new > 0 ? max_new : 1;  // first token comes from prefill
+  ensure_rows(c, B * n);
+  ensure_logits(c, B * n);
+  hipStream_t s = c->stream;
+  if (!c->pstate && persistent_supported(m->pplan, (int)B)) c->pstate = persistent_state_create(m->pplan, c->k, c->v, (int)B, c->token_dev, c->pos_dev, c->logits, c->keys);
+  HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
+  HIPX(hipEventRecord(c->ev[0], s));
+  enqueue_prefill(c, c->ids_in, B, n, 0, 0);
+  // argmax of the last row of each sequence (extract_row(logits, n-1))
+  launch_argmax(s, c->logits + (n - 1) * V, (long)(n * V), (int)B, (int)V, c->keys);
+  set_counters(c, (int)n, 0);
+  launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev);
+  HIPX(hipEventRecord(c->ev[1], s));
+  ensure_graph(c);
+  for (size_t i = 1; i < steps; ++i) HIPX(hipGraphLaunch(c->graph_exec, s));
+  HIPX(hipEventRecord(c->ev[2], s));
+  std::vector<uint32_t> gen(B * P);
+  HIPX(hipMemcpyAsync(gen.data(), c->ids_dev, B * P * 4, hipMemcpyDeviceToHost, s));
+  HIPX(hipStreamSynchronize(s));
+  c->len = n + steps - 1;  // the last generated token is never fed back
+  const size_t outlen = n + steps;
+  for (size_t b = 0; b < B; ++b) {
+    memcpy(out + b * outlen, prompts + b * n, n * 4);
+    memcpy(out + b * outlen + n, gen.data() + b * P, steps * 4);
+  }
+  if (timing) {
+    float a = 0.f, b2 = 0.f;
+    HIPX(hipEventElapsedTime(&a, c->ev[0], c->ev[1]));
+    HIPX(hipEventElapsedTime(&b2, c->ev[1], c->ev[2]));
+    timing->prefill_ms = a;
+    timing->decode_ms = b2;
+    timing->decode_steps = steps - 1;
+    timing->decode_step_kernel_ms = 0.0;
+    timing->decode_step_kernel_launches = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side sampling (gpt2.rs:871-1017), seeded instead of thread_rng.
+// ---------------------------------------------------------------------------
+
+namespace {
+struct SplitMix {
+  uint64_t s;
+  uint64_t next() {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  float uniform() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }  // [0, 1)
+};
+
+uint32_t argmax_host(const float* v, size_t n) {
+  size_t best = 0;
+  float bv = -INFINITY;
+  for (size_t i = 0; i < n; ++i)
+    if (v[i] > bv) {
+      bv = v[i];
+      best = i;
+    }
+  return (uint32_t)best;
+}
+
+void rep_penalty(std::vector<float>& l, const std::vector<uint32_t>& toks, float pen) {
+  for (uint32_t t : toks)
+    if (t < l.size()) l[t] = l[t] > 0.0f ? l[t] / pen : l[t] * pen;
+}
+
+void top_k(std::vector<float>& l, size_t k) {
+  std::vector<float> s(l);
+  std::stable_sort(s.begin(), s.end(), [](float a, float b) { return a > b; });
+  const float thr = s[std::min(k, s.size()) - 1];
+  for (float& v : l)
+    if (v < thr) v = -INFINITY;
+}
+
+std::vector<float> softmax_host(const std::vector<float>& l) {
+  float mx = -INFINITY;
+  for (float v : l) mx = std::fmax(mx, v);
+  std::vector<float> p(l.size());
+  float sum = 0.f;
+  for (size_t i = 0; i < l.size(); ++i) {
+    p[i] = expf(l[i] - mx);
+    sum += p[i];
+  }
+  for (float& v : p) v = v / sum;
+  return p;
+}
+
+void top_p(std::vector<float>& l, float pthr) {
+  std::vector<float> p = softmax_host(l);
+  std::vector<size_t> idx(p.size());
+  std::iota(idx.begin(), idx.end(), 0);
+  std::stable_sort(idx.begin(), idx.end(), [&](size_t a, size_t b) { return p[a] > p[b]; });
+  std::vector<char> keep(p.size(), 0);
+  float cum = 0.f;
+  for (size_t i : idx) {
+    keep[i] = 1;
+    cum += p[i];
+    if (cum >= pthr) break;
+  }
+  for (size_t i = 0; i < l.size(); ++i)
+    if (!keep[i]) l[i] = -INFINITY;
+}
+
+uint32_t sample_from(const std::vector<float>& l, SplitMix& rng) {
+  std::vector<float> p = softmax_host(l);
+  const float r = rng.uniform();
+  float cum = 0.f;
+  for (size_t i = 0; i < p.size(); ++i) {
+    cum += p[i];
+    if (r < cum) return (uint32_t)i;
+  }
+  return (uint32_t)(p.size() - 1);
+}
+
+// sample_logits, gpt2.rs:871-906.
+uint32_t sample_logits(const float* logits, size_t V, const std::vector<uint32_t>& toks, const rtg_gen_config& cfg,
+                       SplitMix& rng) {
+  if (cfg.temperature <= 0.0f) {
+    if (cfg.repetition_penalty != 1.0f) {
+      std::vector<float> mod(logits, logits + V);
+      rep_penalty(mod, toks, cfg.repetition_penalty);
+      return argmax_host(mod.data(), V);
+    }
+    return argmax_host(logits, V);
+  }
+  std::vector<float> mod(logits, logits + V);
+  if (cfg.repetition_penalty != 1.0f) rep_penalty(mod, toks, cfg.repetition_penalty);
+  for (float& v : mod) v /= cfg.temperature;
+  if (cfg.top_k > 0 && cfg.top_k < V) top_k(mod, cfg.top_k);
+  if (cfg.top_p < 1.0f && cfg.top_p > 0.0f) top_p(mod, cfg.top_p);
+  return sample_from(mod, rng);
+}
+
+// sample_with_temperature, gpt2.rs:986-1017.
+uint32_t sample_temperature(const float* logits, size_t V, float temperature, SplitMix& rng) {
+  std::vector<float> mod(logits, logits + V);
+  for (float& v : mod) v = v / temperature;
+  return sample_from(mod, rng);
+}
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Model construction (gpt2.rs:214-263)
+// ---------------------------------------------------------------------------
+
+namespace {
+struct HostTensor {
+  std::vector<size_t> shape;
+  const float* data = nullptr;
+  std::vector<float> owned;
+};
+
+using Lookup = std::map<std::string, HostTensor>;
+
+std::string shape_str(const std::vector<size_t>& s) {
+  std::string r = "[";
+  for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+  return r + "]";
+}
+
+rtg_result build_model(const rtg_config* cfg, Lookup& lk, rtg_storage storage, rtg_model** out) {
+  const size_t d = cfg->n_embd, L = cfg->n_layer, V = cfg->vocab_size, P = cfg->n_positions, H = cfg->n_head;
+  // gpt2.rs:224-263: look up every name first, in the reference's order.
+  std::vector<std::string> names = {"wte.weight", "wpe.weight", "ln_f.weight", "ln_f.bias"};
+  const char* per[] = {"ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias",
+                       "attn.c_proj.weight", "attn.c_proj.bias", "ln_2.weight", "ln_2.bias",
+                       "mlp.c_fc.weight", "mlp.c_fc.bias", "mlp.c_proj.weight", "mlp.c_proj.bias"};
+  for (size_t i = 0; i < L; ++i)
+    for (const char* p : per) names.push_back("h." + std::to_string(i) + "." + p);
+  for (const auto& nm : names)
+    if (!lk.count(nm)) return err("Missing weight: " + nm);
+  if (H == 0 || d == 0 || d % H != 0) return err(fmt("n_embd %zu is not divisible by n_head %zu", d, H));
+  const size_t hd = d / H;
+  if (hd > 64) return err(fmt("head_dim %zu > 64 is not supported", hd));
+  if (d % 8 != 0) return err(fmt("n_embd %zu must be a multiple of 8", d));
+  // Shapes (the reference does not check them; a mismatch there is a panic or garbage).
+  auto want = [&](const std::string& nm, std::vector<size_t> s) -> std::string {
+    const auto& t = lk[nm];
+    if (t.shape != s) return "Shape mismatch for " + nm + ": expected " + shape_str(s) + ", got " + shape_str(t.shape);
+    return "";
+  };
+  std::string e;
+  if (!(e = want("wte.weight", {V, d})).empty() || !(e = want("wpe.weight", {P, d})).empty() ||
+      !(e = want("ln_f.weight", {d})).empty() || !(e = want("ln_f.bias", {d})).empty())
+    return err(e);
+  for (size_t i = 0; i < L; ++i) {
+    std::string p = "h." + std::to_string(i) + ".";
+    std::vector<std::pair<const char*, std::vector<size_t>>> sh = {
+        {"ln_1.weight", {d}}, {"ln_1.bias", {d}}, {"attn.c_attn.weight", {d, 3 * d}}, {"attn.c_attn.bias", {3 * d}},
+        {"attn.c_proj.weight", {d, d}}, {"attn.c_proj.bias", {d}}, {"ln_2.weight", {d}}, {"ln_2.bias", {d}},
+        {"mlp.c_fc.weight", {d, 4 * d}}, {"mlp.c_fc.bias", {4 * d}}, {"mlp.c_proj.weight", {4 * d, d}},
+        {"mlp.c_proj.bias", {d}}};
+    for (auto& kv : sh)
+      if (!(e = want(p + kv.first, kv.second)).empty()) return err(e);
+  }
+  std::string derr = check_device();
+  if (!derr.empty()) return err(derr);
+
+  std::unique_ptr<rtg_model> m(new rtg_model());
+  m->cfg = *cfg;
+  m->hd = (int)hd;
+  m->wtype = storage == RTG_STORE_BF16 ? W_BF16 : W_F32;
+  hipGetDevice(&m->device);
+  const size_t wb = m->wtype == W_BF16 ? 2 : 4;
+  // Arena layout: per layer [wqkv wproj wfc wmproj | biases | LN], then wte, wpe, ln_f.
+  std::vector<size_t> offs;
+  size_t cur = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = cur;
+    cur = align_up(cur + bytes, 256);
+    return o;
+  };
+  struct LOff {
+    size_t wqkv, waproj, wfc, wmproj, bqkv, baproj, bfc, bmproj, ln1w, ln1b, ln2w, ln2b;
+  };
+  std::vector<LOff> lo(L);
+  for (size_t i = 0; i < L; ++i) {
+    lo[i].wqkv = take(3 * d * d * wb);
+    lo[i].waproj = take(d * d * wb);
+    lo[i].wfc = take(4 * d * d * wb);
+    lo[i].wmproj = take(4 * d * d * wb);
+    lo[i].bqkv = take(3 * d * 4);
+    lo[i].baproj = take(d * 4);
+    lo[i].bfc = take(4 * d * 4);
+    lo[i].bmproj = take(d * 4);
+    lo[i].ln1w = take(d * 4);
+    lo[i].ln1b = take(d * 4);
+    lo[i].ln2w = take(d * 4);
+    lo[i].ln2b = take(d * 4);
+  }
+  const size_t o_wte = take(V * d * wb), o_wpe = take(P * d * 4), o_lnfw = take(d * 4), o_lnfb = take(d * 4);
+  float* staging = nullptr;
+  try {
+    HIPX(hipMalloc(&m->arena, cur));
+    m->arena_bytes = cur;
+    char* A = reinterpret_cast<char*>(m->arena);
+    size_t stage_max = std::max({V * d, P * d, 4 * d * d});
+    HIPX(hipMalloc(&staging, stage_max * 4));
+    hipStream_t s = nullptr;
+    auto upload_f32 = [&](const std::string& nm, size_t off) {
+      const auto& t = lk[nm];
+      size_t n = 1;
+      for (size_t x : t.shape) n *= x;
+      HIPX(hipMemcpy(A + off, t.data, n * 4, hipMemcpyHostToDevice));
+    };
+    auto upload_wt = [&](const std::string& nm, size_t off) {  // [K][N] -> W^T [N][K] in storage type
+      const auto& t = lk[nm];
+      const size_t K = t.shape[0], N = t.shape[1];
+      HIPX(hipMemcpy(staging, t.data, K * N * 4, hipMemcpyHostToDevice));
+      launch_transpose_to(s, staging, (int)K, (int)N, A + off, m->wtype);
+      HIPX(hipGetLastError());
+      HIPX(hipDeviceSynchronize());
+    };
+    m->layers.resize(L);
+    for (size_t i = 0; i < L; ++i) {
+      std::string p = "h." + std::to_string(i) + ".";
+      upload_wt(p + "attn.c_attn.weight", lo[i].wqkv);
+      upload_wt(p + "attn.c_proj.weight", lo[i].waproj);
+      upload_wt(p + "mlp.c_fc.weight", lo[i].wfc);
+      upload_wt(p + "mlp.c_proj.weight", lo[i].wmproj);
+      upload_f32(p + "attn.c_attn.bias", lo[i].bqkv);
+      upload_f32(p + "attn.c_proj.bias", lo[i].baproj);
+      upload_f32(p + "mlp.c_fc.bias", lo[i].bfc);
+      upload_f32(p + "mlp.c_proj.bias", lo[i].bmproj);
+      upload_f32(p + "ln_1.weight", lo[i].ln1w);
+      upload_f32(p + "ln_1.bias", lo[i].ln1b);
+      upload_f32(p + "ln_2.weight", lo[i].ln2w);
+      upload_f32(p + "ln_2.bias", lo[i].ln2b);
+      LayerW& w = m->layers[i];
+      w.wqkv = A + lo[i].wqkv;
+      w.waproj = A + lo[i].waproj;
+      w.wfc = A + lo[i].wfc;
+      w.wmproj = A + lo[i].wmproj;
+      w.bqkv = reinterpret_cast<float*>(A + lo[i].bqkv);
+      w.baproj = reinterpret_cast<float*>(A + lo[i].baproj);
+      w.bfc = reinterpret_cast<float*>(A + lo[i].bfc);
+      w.bmproj = reinterpret_cast<float*>(A + lo[i].bmproj);
+      w.ln1w = reinterpret_cast<float*>(A + lo[i].ln1w);
+      w.ln1b = reinterpret_cast<float*>(A + lo[i].ln1b);
+      w.ln2w = reinterpret_cast<float*>(A + lo[i].ln2w);
+      w.ln2b = reinterpret_cast<float*>(A + lo[i].ln2b);
+    }
+    {
+      const auto& t = lk["wte.weight"];
+      HIPX(hipMemcpy(staging, t.data, V * d * 4, hipMemcpyHostToDevice));
+      launch_convert_to(s, staging, (long)(V * d), A + o_wte, m->wtype);
+      HIPX(hipGetLastError());
+      HIPX(hipDeviceSynchronize());
+    }
+    upload_f32("wpe.weight", o_wpe);
+    upload_f32("ln_f.weight", o_lnfw);
+    upload_f32("ln_f.bias", o_lnfb);
+    m->wte = A + o_wte;
+    m->wpe = reinterpret_cast<float*>(A + o_wpe);
+    m->lnfw = reinterpret_cast<float*>(A + o_lnfw);
+    m->lnfb = reinterpret_cast<float*>(A + o_lnfb);
+    HIPX(hipFree(staging));
+    staging = nullptr;
+  } catch (const HipError& he) {
+    if (staging) hipFree(staging);
+    return err(he.msg);
+  }
+  size_t np = V * d + P * d + 2 * d;
+  np += L * (2 * d + d * 3 * d + 3 * d + d * d + d + 2 * d + d * 4 * d + 4 * d + 4 * d * d + d);
+  m->nparams = np;
+  {
+    PersistentWeights pw;
+    pw.cfg = m->cfg;
+    pw.wtype = m->wtype;
+    pw.wte = m->wte;
+    pw.wpe = m->wpe;
+    pw.lnfw = m->lnfw;
+    pw.lnfb = m->lnfb;
+    for (auto& l : m->layers)
+      pw.layers.push_back({l.wqkv, l.waproj, l.wfc, l.wmproj, l.bqkv, l.baproj, l.bfc, l.bmproj, l.ln1w, l.ln1b,
+                           l.ln2w, l.ln2b});
+    m->pplan = persistent_plan_create(pw);
+  }
+  *out = m.release();
+  return ok();
+}
+
+bool decode_to_f32(const void* data, rtg_dtype dt, size_t n, std::vector<float>* out) {
+  out->resize(n);
+  const uint8_t* raw = reinterpret_cast<const uint8_t*>(data);
+  switch (dt) {
+    case RTG_F32: memcpy(out->data(), data, n * 4); return true;
+    case RTG_BF16:
+      for (size_t i = 0; i < n; ++i) {
+        uint32_t b = (uint32_t)(raw[2 * i] | (raw[2 * i + 1] << 8)) << 16;
+        memcpy(&(*out)[i], &b, 4);
+      }
+      return true;
+    case RTG_F64:
+      for (size_t i = 0; i < n; ++i) {
+        double v;
+        memcpy(&v, raw + 8 * i, 8);
+        (*out)[i] = (float)v;
+      }
+      return true;
+    case RTG_F16: {
+      rtg::StFile f;
+      rtg::StEntry e;
+      e.dtype = "F16";
+      e.shape = {n};
+      e.begin = 0;
+      e.end = 2 * n;
+      f.bytes.assign(raw, raw + 2 * n);
+      f.data_start = 0;
+      return rtg::st_decode_f32(f, e, out).empty();
+    }
+  }
+  return false;
+}
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+extern "C" {
+
+void rtg_init(void) { hipInit(0); }
+void rtg_cleanup(void) {}
+const char* rtg_version(void) { return "rtgpu 0.1.0 (gfx950)"; }
+
+void rtg_free_error_message(char* msg) { free(msg); }
+
+rtg_result rtg_model_from_host(const rtg_config* cfg, const rtg_named_tensor* tensors, size_t n, rtg_storage storage,
+                               rtg_model** out) {
+  if (!cfg || !out) return err("null argument");
+  Lookup lk;
+  for (size_t i = 0; i < n; ++i) {
+    const rtg_named_tensor& t = tensors[i];
+    HostTensor h;
+    h.shape.assign(t.shape, t.shape + t.ndim);
+    size_t numel = 1;
+    for (size_t s : h.shape) numel *= s;
+    if (t.dtype == RTG_F32) {
+      h.data = reinterpret_cast<const float*>(t.data);
+    } else {
+      if (!decode_to_f32(t.data, t.dtype, numel, &h.owned)) return err("Unsupported dtype for " + std::string(t.name));
+      h.data = h.owned.data();
+    }
+    lk[t.name] = std::move(h);
+    if (lk[t.name].owned.size()) lk[t.name].data = lk[t.name].owned.data();
+  }
+  return build_model(cfg, lk, storage, out);
+}
+
+rtg_result rtg_model_from_safetensors(const char* path, const rtg_config* cfg, rtg_storage storage,
+                                      rtg_model** out) {
+  if (!cfg || !out || !path) return err("null argument");
+  StFile f;
+  std::string e = st_read_file(path, &f);
+  if (!e.empty()) return err("Failed to load safetensors: " + e);
+  Lookup lk;
+  for (auto& kv : f.entries) {
+    HostTensor h;
+    h.shape = kv.second.shape;
+    e = st_decode_f32(f, kv.second, &h.owned);
+    if (!e.empty()) return err("Failed to load safetensors: " + e);
+    lk[kv.first] = std::move(h);
+    lk[kv.first].data = lk[kv.first].owned.data();
+  }
+  f.bytes.clear();
+  f.bytes.shrink_to_fit();
+  return build_model(cfg, lk, storage, out);
+}
+
+void rtg_model_destroy(rtg_model* model) { delete model; }
+
+size_t rtg_num_parameters(const rtg_model* model) { return model ? model->nparams : 0; }
+
+rtg_result rtg_cache_new(const rtg_model* model, size_t batch, rtg_cache** out) {
+  if (!model || !out) return err("null argument");
+  if (batch == 0) return err("batch must be >= 1");
+  try {
+    *out = cache_create(model, batch);
+  } catch (const HipError& e) {
+    return err(e.msg);
+  }
+  return ok();
+}
+
+size_t rtg_cache_len(const rtg_cache* cache) { return cache ? cache->len : 0; }
+bool rtg_cache_is_empty(const rtg_cache* cache) { return rtg_cache_len(cache) == 0; }
+void rtg_cache_clear(rtg_cache* cache) {
+  if (cache) cache->len = 0;
+}
+
+void rtg_cache_destroy(rtg_cache* c) {
+  if (!c) return;
+  if (c->stream) hipStreamSynchronize(c->stream);
+  destroy_graph(c);
+  if (c->pstate) persistent_state_destroy(c->pstate);
+  free_work(c);
+  for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
+                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->logits})
+    if (p) hipFree(p);
+  for (auto e : c->ev)
+    if (e) hipEventDestroy(e);
+  if (c->stream) hipStreamDestroy(c->stream);
+  delete c;
+}
+
+rtg_result rtg_cache_read(const rtg_cache* c, size_t layer, size_t head, size_t seq, int values, float* out) {
+  if (!c || !out) return err("null argument");
+  const rtg_model* m = c->m;
+  if (layer >= m->cfg.n_layer || head >= m->cfg.n_head || seq >= c->batch) return err("index out of range");
+  const size_t P = m->cfg.n_positions, hd = m->hd;
+  const float* base = (values ? c->v : c->k) + layer * c->layer_stride + ((seq * m->cfg.n_head + head) * P) * hd;
+  try {
+    if (c->len) HIPX(hipMemcpy(out, base, c->len * hd * 4, hipMemcpyDeviceToHost));
+  } catch (const HipError& e) {
+    return err(e.msg);
+  }
+  return ok();
+}
+
+rtg_result rtg_forward_cached_batched(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
+                                      float* logits_out) {
+  if (!model || !cache) return err("null argument");
+  std::string e = check_cached(model, cache->len, ids, n);
+  if (e.empty() && cache->batch > 1) e = check_ids(model, ids, n * cache->batch);
+  if (!e.empty()) return err(e);
+  try {
+    forward_cached_impl(cache, ids, n, logits_out);
+  } catch (const HipError& he) {
+    return err(he.msg);
+  }
+  return ok();
+}
+
+rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
+                              float* logits_out) {
+  if (cache && cache->batch != 1) return err("rtg_forward_cached needs a batch-1 cache");
+  return rtg_forward_cached_batched(model, cache, ids, n, logits_out);
+}
+
+rtg_result rtg_forward(const rtg_model* model, const uint32_t* ids, size_t n, float* logits_out) {
+  if (!model) return err("null argument");
+  // gpt2.rs:269-279
+  if (n == 0) return err("Empty input");
+  if (n > model->cfg.n_positions)
+    return err(fmt("Sequence length %zu exceeds max position %zu", n, model->cfg.n_positions));
+  std::string e = check_ids(model, ids, n);
+  if (!e.empty()) return err(e);
+  try {
+    PoolLease lease(model, 1);
+    forward_cached_impl(lease.c, ids, n, logits_out);
+  } catch (const HipError& he) {
+    return err(he.msg);
+  }
+  return ok();
+}
+
+rtg_result rtg_generate_cached_batched(const rtg_model* model, const uint32_t* prompts, size_t batch, size_t n,
+                                       size_t max_new, uint32_t* out, rtg_timing* timing) {
+  if (!model || !out) return err("null argument");
+  if (batch == 0) return err("batch must be >= 1");
+  const size_t P = model->cfg.n_positions;
+  std::string e = check_cached(model, 0, prompts, n);
+  if (e.empty() && batch > 1) e = check_ids(model, prompts, n * batch);
+  if (!e.empty()) return err(e);
+  // The reference fails at the first decode step whose total exceeds
+  // n_positions and discards the partial result (gpt2.rs:369-374, 427-433).
+  const size_t steps = max_new > 0 ? max_new : 1;
+  if (n + steps - 1 > P) return err(fmt("Total sequence length %zu exceeds max position %zu", P + 1, P));
+  try {
+    generate_greedy(model, prompts, batch, n, max_new, out, timing);
+  } catch (const HipError& he) {
+    return err(he.msg);
+  }
+  return ok();
+}
+
+rtg_result rtg_generate_cached(const rtg_model* model, const uint32_t* prompt, size_t n, size_t max_new,
+                               float temperature, uint64_t seed, uint32_t* out) {
+  if (temperature <= 0.0f) return rtg_generate_cached_batched(model, prompt, 1, n, max_new, out, nullptr);
+  if (!model || !out) return err("null argument");
+  // Sampling path (gpt2.rs:405-441 with sample_with_temperature).
+  std::string e = check_cached(model, 0, prompt, n);
+  if (!e.empty()) return err(e);
+  const size_t V = model->cfg.vocab_size, P = model->cfg.n_positions;
+  const size_t steps = max_new > 0 ? max_new : 1;
+  if (n + steps - 1 > P) return err(fmt("Total sequence length %zu exceeds max position %zu", P + 1, P));
+  SplitMix rng{seed};
+  try {
+    PoolLease lease(model, 1);
+    rtg_cache* c = lease.c;
+    std::vector<float> logits(n * V);
+    forward_cached_impl(c, prompt, n, logits.data());
+    std::vector<uint32_t> toks(prompt, prompt + n);
+    toks.push_back(sample_temperature(logits.data() + (n - 1) * V, V, temperature, rng));
+    for (size_t i = 1; i < steps; ++i) {
+      uint32_t last = toks.back();
+      forward_cached_impl(c, &last, 1, logits.data());
+      toks.push_back(sample_temperature(logits.data(), V, temperature, rng));
+    }
+    memcpy(out, toks.data(), toks.size() * 4);
+  } catch (const HipError& he) {
+    return err(he.msg);
+  }
+  return ok();
+}
+
+rtg_result rtg_generate_with_config(const rtg_model* model, const uint32_t* prompt, size_t n,
+                                    const rtg_gen_config* cfg, uint32_t* out) {
+  if (!model || !out || !cfg) return err("null argument");
+  if (cfg->temperature <= 0.0f && cfg->repetition_penalty == 1.0f)
+    return rtg_generate_cached_batched(model, prompt, 1, n, cfg->max_new_tokens, out, nullptr);
+  std::string e = check_cached(model, 0, prompt, n);
+  if (!e.empty()) return err(e);
+  const size_t V = model->cfg.vocab_size, P = model->cfg.n_positions;
+  const size_t steps = cfg->max_new_tokens > 0 ? cfg->max_new_tokens : 1;
+  if (n + steps - 1 > P) return err(fmt("Total sequence length %zu exceeds max position %zu", P + 1, P));
+  SplitMix rng{cfg->seed};
+  try {
+    PoolLease lease(model, 1);
+    rtg_cache* c = lease.c;
+    std::vector<float> logits(n * V);
+    forward_cached_impl(c, prompt, n, logits.data());
+    std::vector<uint32_t> toks(prompt, prompt + n);
+    toks.push_back(sample_logits(logits.data() + (n - 1) * V, V, toks, *cfg, rng));
+    for (size_t i = 1; i < steps; ++i) {
+      uint32_t last = toks.back();
+      forward_cached_impl(c, &last, 1, logits.data());
+      toks.push_back(sample_logits(logits.data(), V, toks, *cfg, rng));
+    }
+    memcpy(out, toks.data(), toks.size() * 4);
+  } catch (const HipError& he) {
+    return err(he.msg);
+  }
+  return ok();
+}
+
+rtg_result rtg_generate(const rtg_model* model, const uint32_t* prompt, size_t n, size_t max_new, float temperature,
+                        uint64_t seed, uint32_t* out) {
+  if (!model || !out) return err("null argument");
+  // gpt2.rs:311-346: each step runs forward() over the last n_positions tokens.
+  const size_t V = model->cfg.vocab_size, P = model->cfg.n_positions;
+  std::vector<uint32_t> toks(prompt, prompt + n);
+  SplitMix rng{seed};
+  try {
+    PoolLease lease(model, 1);
+    rtg_cache* c = lease.c;
+    for (size_t i = 0; i < max_new; ++i) {
+      const size_t start = toks.size() > P ? toks.size() - P : 0;
+      const size_t ctx = toks.size() - start;
+      if (ctx == 0) return err("Empty input");
+      std::string e = check_ids(model, toks.data() + start, ctx);
+      if (!e.empty()) return err(e);
+      c->len = 0;
+      ensure_rows(c, ctx);
+      ensure_logits(c, 1);
+      HIPX(hipMemcpyAsync(c->ids_in, toks.data() + start, ctx * 4, hipMemcpyHostToDevice, c->stream));
+      enqueue_prefill(c, c->ids_in, 1, ctx, 0, 1);  // logits of the last row only
+      std::vector<float> row(V);
+      HIPX(hipMemcpyAsync(row.data(), c->logits, V * 4, hipMemcpyDeviceToHost, c->stream));
+      HIPX(hipStreamSynchronize(c->stream));
+      toks.push_back(temperature <= 0.0f ? argmax_host(row.data(), V)
+                                         : sample_temperature(row.data(), V, temperature, rng));
+    }
+    c->len = 0;
+  } catch (const HipError& he) {
+    return err(he.msg);
+  }
+  memcpy(out, toks.data(), toks.size() * 4);
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,238 @@
+"""GPU parity: librtgpu.so (through its C ABI) against the CPU oracle.
+
+Bar (from the task's north star): logits within |d| <= 1e-3 + 1e-4 |ref|;
+greedy ids identical. Oracle sizes are chosen so the CPU side finishes in
+seconds; full-size configs are covered by size-independent properties
+(batch independence, cached == uncached, determinism) elsewhere.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from rusttorch_amd import synth
+from rusttorch_amd.gpt2 import Gpt2Config, Gpt2Error, Gpt2Model, GenerationConfig
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+ATOL, RTOL = 1e-3, 1e-4
+
+
+def assert_logits_close(got, ref, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref) - (ATOL + RTOL * np.abs(ref))
+    worst = float(np.max(err))
+    assert worst <= 0, f"{what}: max excess {worst:.3e}, max abs diff {np.max(np.abs(got - ref)):.3e}"
+
+
+def cfg_of(sh):
+    return Gpt2Config(sh.vocab_size, sh.n_positions, sh.n_embd, sh.n_layer, sh.n_head, sh.layer_norm_epsilon)
+
+
+@pytest.fixture(scope="module")
+def O(oracle_lib):
+    return oracle_lib
+
+
+_models = {}
+
+
+def gpu_model(name, storage="f32"):
+    key = (name, storage)
+    if key not in _models:
+        from tests.golden.make_golden import build_case
+        if name in ("tiny_const", "tiny_rand", "mini"):
+            sd, sh, _ = build_case(name)
+        else:
+            sh = synth.SHAPES[name]
+            sd = synth.make_weights(sh, bf16=(storage == "bf16"))
+        print(f"[gpu] loading model {name} storage={storage}", flush=True)
+        _models[key] = (sd, sh, Gpt2Model.from_state_dict(sd, cfg_of(sh), storage=storage))
+    return _models[key]
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures (tiny reference model, tiny random, mini)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["tiny_const", "tiny_rand", "mini"])
+def test_golden_prefill_and_decode(name):
+    g = np.load(os.path.join(GOLDEN, f"{name}.npz"), allow_pickle=False)
+    sd, sh, m = gpu_model(name)
+    prompt = g["prompt"]
+    cache = m.new_cache()
+    rows = [m.forward_cached(prompt, cache)[-1]]
+    toks = list(prompt) + [int(np.argmax(rows[-1]))]
+    for _ in range(int(g["decode_steps"])):
+        rows.append(m.forward_cached([toks[-1]], cache)[0])
+        toks.append(int(np.argmax(rows[-1])))
+    assert_logits_close(np.stack(rows), g["logits"], name)
+    assert cache.len() == len(prompt) + int(g["decode_steps"])
+    assert m.generate_cached(prompt, int(g["n_greedy"]), 0.0) == g["greedy_ids"].tolist()
+
+
+def test_cache_contents_match_oracle(O):
+    sd, sh, m = gpu_model("mini")
+    ids = synth.make_tokens(20, sh.vocab_size, stream=3)
+    c = m.new_cache()
+    m.forward_cached(ids[:12], c)
+    for t in range(12, 20):
+        m.forward_cached(ids[t:t + 1], c)
+    om = O.OracleModel.from_shape(sd, sh)
+    oc = om.new_cache()
+    om.forward_cached(ids, oc)
+    for layer in range(sh.n_layer):
+        for head in range(sh.n_head):
+            for values in (False, True):
+                np.testing.assert_allclose(c.read(layer, head, values=values), oc.read(layer, head, values=values),
+                                           atol=1e-4, rtol=1e-4)
+
+
+# ---------------------------------------------------------------------------
+# rusttorch's own GPT-2 tests, on the GPU (gpt2.rs:1103-1648)
+# ---------------------------------------------------------------------------
+
+def test_reference_shapes_and_errors():
+    _, sh, m = gpu_model("tiny_const")
+    assert m.forward([0, 1, 2]).shape == (3, 10)
+    assert m.forward([0]).shape == (1, 10)
+    with pytest.raises(Gpt2Error, match="^Empty input$"):
+        m.forward([])
+    with pytest.raises(Gpt2Error, match="^Sequence length 20 exceeds max position 16$"):
+        m.forward(list(range(20)))
+    with pytest.raises(Gpt2Error, match=r"^Token ID 10 out of range \(vocab_size=10\)$"):
+        m.forward([1, 10])
+    assert len(m.generate([0, 1], 3, 0.0)) == 5
+    assert len(m.generate_cached([0, 1, 2], 7, 0.0)) == 10
+    assert len(m.generate_cached([0, 1, 2], 0, 0.0)) == 4
+    assert m.num_parameters() == synth.num_parameters(sh)
+
+
+def test_reference_cache_bookkeeping():
+    _, _, m = gpu_model("tiny_const")
+    c = m.new_cache()
+    assert c.len() == 0 and c.is_empty()
+    m.forward_cached([0, 1, 2], c)
+    assert c.len() == 3
+    m.forward_cached([3], c)
+    assert c.len() == 4
+    c.clear()
+    assert c.is_empty()
+    m.forward_cached([i % 10 for i in range(15)], c)
+    m.forward_cached([0], c)
+    assert c.len() == 16
+    with pytest.raises(Gpt2Error, match="^Total sequence length 17 exceeds max position 16$"):
+        m.forward_cached([0], c)
+    assert c.len() == 16
+    c.clear()
+    with pytest.raises(Gpt2Error, match="^Empty input$"):
+        m.forward_cached([], c)
+    with pytest.raises(Gpt2Error, match="^Total sequence length 17 exceeds max position 16$"):
+        m.forward_cached([99] * 17, c)
+    with pytest.raises(Gpt2Error, match=r"^Token ID 99 out of range \(vocab_size=10\)$"):
+        m.forward_cached([1, 99], c)
+    assert c.len() == 0
+
+
+@pytest.mark.parametrize("name", ["tiny_const", "tiny_rand", "mini"])
+def test_reference_self_consistency(name):
+    _, sh, m = gpu_model(name)
+    toks = synth.make_tokens(5, sh.vocab_size, stream=11).tolist()
+    full = m.forward(toks)
+    c = m.new_cache()
+    assert np.max(np.abs(m.forward_cached(toks, c)[-1] - full[-1])) < 1e-4
+    c = m.new_cache()
+    m.forward_cached(toks[:3], c)
+    assert np.max(np.abs(m.forward_cached(toks[3:], c)[1] - full[-1])) < 1e-4
+    c = m.new_cache()
+    for t in toks[:-1]:
+        m.forward_cached([t], c)
+    assert np.max(np.abs(m.forward_cached([toks[-1]], c)[0] - full[-1])) < 1e-4
+    assert m.generate(toks[:2], 5, 0.0) == m.generate_cached(toks[:2], 5, 0.0)
+    assert m.generate_with_config(toks[:2], GenerationConfig.greedy(5)) == m.generate_cached(toks[:2], 5, 0.0)
+
+
+def test_generate_sliding_window(O):
+    sd, sh, m = gpu_model("tiny_rand")
+    om = O.OracleModel.from_shape(sd, sh)
+    prompt = [1, 2, 3]
+    assert m.generate(prompt, 20, 0.0) == om.generate(prompt, 20)  # crosses n_positions = 16
+
+
+def test_sampling_paths():
+    _, sh, m = gpu_model("mini")
+    p = synth.make_tokens(8, sh.vocab_size).tolist()
+    cfg = GenerationConfig.creative(6)
+    cfg.seed = 42
+    a = m.generate_with_config(p, cfg)
+    assert a == m.generate_with_config(p, cfg) and len(a) == 14 and max(a) < sh.vocab_size
+    b = m.generate_cached(p, 6, 1.0, seed=7)
+    assert b == m.generate_cached(p, 6, 1.0, seed=7) and len(b) == 14
+    # repetition penalty on the greedy path
+    g = GenerationConfig.greedy(6)
+    g.repetition_penalty = 1.3
+    out = m.generate_with_config(p, g)
+    assert len(out) == 14
+
+
+# ---------------------------------------------------------------------------
+# GPT-2 small: configuration c1 (prompt 32, greedy 64) and a slice of c2
+# ---------------------------------------------------------------------------
+
+def test_small_c1_logits_and_ids(O):
+    sd, sh, m = gpu_model("small")
+    prompt = synth.make_tokens(32, sh.vocab_size)
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    print("[gpu] c1 oracle generate", flush=True)
+    ref_ids = om.generate_cached(prompt, 64)
+    ids = m.generate_cached(prompt, 64, 0.0)
+    assert ids == ref_ids
+    # logits of the prefill and the first 8 decode steps, step by step
+    c, oc = m.new_cache(), om.new_cache()
+    assert_logits_close(m.forward_cached(prompt, c), om.forward_cached(prompt, oc), "c1 prefill")
+    for t in range(32, 40):
+        tok = [ref_ids[t]]
+        assert_logits_close(m.forward_cached(tok, c), om.forward_cached(tok, oc), f"c1 step {t}")
+
+
+def test_small_batched_matches_single(O):
+    sd, sh, m = gpu_model("small")
+    B, n, steps = 8, 128, 256
+    prompts = np.stack([synth.make_tokens(n, sh.vocab_size, stream=100 + b) for b in range(B)])
+    out = m.generate_cached_batched(prompts, steps)
+    assert out.shape == (B, n + steps)
+    for b in (0, 5):
+        assert out[b].tolist() == m.generate_cached(prompts[b], steps, 0.0)
+    # oracle on a slice: 2 sequences, 12 greedy tokens
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    for b in (0, 7):
+        assert om.generate_cached(prompts[b], 12) == out[b, : n + 12].tolist()
+
+
+def test_batched_forward_logits(O):
+    sd, sh, m = gpu_model("mini")
+    B, n = 3, 10
+    prompts = np.stack([synth.make_tokens(n, sh.vocab_size, stream=200 + b) for b in range(B)])
+    c = m.new_cache(batch=B)
+    lg = m.forward_cached_batched(prompts, c)
+    om = O.OracleModel.from_shape(sd, sh)
+    for b in range(B):
+        assert_logits_close(lg[b], om.forward(prompts[b]), f"batched seq {b}")
+    nxt = prompts[:, :1]
+    lg2 = m.forward_cached_batched(nxt, c)
+    for b in range(B):
+        oc = om.new_cache()
+        om.forward_cached(prompts[b], oc)
+        assert_logits_close(lg2[b], om.forward_cached(nxt[b], oc), f"batched step seq {b}")
+
+
+def test_bf16_storage_matches_oracle(O):
+    sh = synth.SHAPES["mini"]
+    sd = synth.make_weights(sh, bf16=True)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh), storage="bf16")
+    om = O.OracleModel.from_shape(sd, sh)
+    ids = synth.make_tokens(24, sh.vocab_size, stream=5)
+    assert_logits_close(m.forward(ids), om.forward(ids), "bf16 forward")
+    assert m.generate_cached(ids[:8], 30, 0.0) == om.generate_cached(ids[:8], 30)
