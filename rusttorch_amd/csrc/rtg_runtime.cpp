@@ -375,7 +375,9 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   enqueue_prefill(c, c->ids_in, B, n, 0, 0);
   // argmax of the last row of each sequence (extract_row(logits, n-1))
   launch_argmax(s, c->logits + (n - 1) * V, (long)(n * V), (int)B, (int)V, c->keys);
-  set_counters(c, (int)n, 0);
+  // finalize advances pos by one: after it, pos = n, the position of the
+  // prefill token that the first decode step consumes.
+  set_counters(c, (int)n - 1, 0);
   launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev);
   HIPX(hipEventRecord(c->ev[1], s));
   ensure_graph(c);
