@@ -113,10 +113,12 @@ def main():
     step_bytes = [decode_bytes(sh, B, n_prompt + i, wbytes) for i in range(n_new - 1)]
     avg_bytes = float(np.mean(step_bytes))
     step_ms = dec_ms / dec_steps
-    kern_ms = sum(t["decode_step_kernel_ms"] for t in tims)
-    kern_n = sum(t["decode_step_kernel_launches"] for t in tims)
+    # the decode-step kernel itself, timed launch by launch (HIP events on its stream)
+    _, prof = m.generate_cached_batched(prompts, n_new, timing=True, profile_kernels=True)
+    kern_ms = prof["decode_kernel_ms"]
+    kern_n = prof["decode_kernel_launches"]
     if kern_n:
-        kernel = "rtg_decode_step (persistent, one launch per decode step)"
+        kernel = "decode_step_kernel (persistent, one launch per decode step)"
         dur_ms = kern_ms / kern_n
     else:
         kernel = "decode step (graph of per-op kernels)"

@@ -77,13 +77,18 @@ typedef struct {
 typedef struct rtg_model rtg_model;
 typedef struct rtg_cache rtg_cache;
 
-/* Device-event timings of the last generate call made with this struct. */
+/* Device-event timings of a generate call (HIP events on the cache's stream).
+ * profile_kernels is an input: when nonzero and the decode step is the single
+ * persistent kernel, the decode steps are replayed once more launch by launch
+ * (identical inputs and results) with events around that kernel, filling
+ * decode_kernel_ms / decode_kernel_launches. */
 typedef struct {
+  int profile_kernels;
   double prefill_ms;     /* forward_cached over the prompt + first argmax */
   double decode_ms;      /* the (max_new - 1) single-token steps */
   size_t decode_steps;
-  double decode_step_kernel_ms; /* summed duration of the dominant decode kernel */
-  size_t decode_step_kernel_launches;
+  double decode_kernel_ms;       /* summed duration of the decode-step kernel */
+  size_t decode_kernel_launches;
 } rtg_timing;
 
 /* rusttorch_init / rusttorch_cleanup / rusttorch_version, ffi/mod.rs:24-48. */

@@ -50,11 +50,12 @@ class NamedTensor(C.Structure):
 
 class Timing(C.Structure):
     _fields_ = [
+        ("profile_kernels", C.c_int),
         ("prefill_ms", C.c_double),
         ("decode_ms", C.c_double),
         ("decode_steps", C.c_size_t),
-        ("decode_step_kernel_ms", C.c_double),
-        ("decode_step_kernel_launches", C.c_size_t),
+        ("decode_kernel_ms", C.c_double),
+        ("decode_kernel_launches", C.c_size_t),
     ]
 
 

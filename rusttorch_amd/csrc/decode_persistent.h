@@ -1,4 +1,5 @@
-// Persistent single-launch decode step (one kernel per generated token).
+// Persistent single-launch decode step (one kernel per generated token) for
+// batch 1; see decode_persistent.hip for the design.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -32,6 +33,10 @@ PersistentState* persistent_state_create(PersistentPlan* p, float* kcache, float
                                          uint32_t* token_dev, int* pos_dev, float* logits,
                                          unsigned long long* keys);
 void persistent_state_destroy(PersistentState* s);
-void persistent_decode_step(PersistentState* s, hipStream_t stream);
+// Enqueue one decode step (reads *token_dev / *pos_dev, writes logits and the
+// packed argmax key). The caller's finalize kernel must advance *epoch.
+hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative);
+unsigned* persistent_epoch(PersistentState* s);
+unsigned* persistent_err(PersistentState* s);
 
 }  // namespace rtg

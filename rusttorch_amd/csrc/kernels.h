@@ -54,9 +54,9 @@ void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const flo
 // Greedy argmax over rows of logits (gpt2.rs:858-868) into packed keys.
 void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V, unsigned long long* keys);
 // Decode bookkeeping: token[b] = unpack(keys[b]); ids_out[b*ld + *step_dev] = token;
-// keys reset; *pos_dev += 1; *step_dev += 1.
+// keys reset; *pos_dev += 1; *step_dev += 1; *epoch += 1 when given.
 void launch_finalize(hipStream_t s, int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
-                     int* pos_dev, int* step_dev);
+                     int* pos_dev, int* step_dev, unsigned* epoch = nullptr);
 // Extract tokens from keys without touching counters (prefill).
 void launch_keys_to_tokens(hipStream_t s, int B, unsigned long long* keys, uint32_t* token);
 void launch_reset_keys(hipStream_t s, int B, unsigned long long* keys);

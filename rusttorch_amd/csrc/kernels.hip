@@ -371,7 +371,7 @@ void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V,
 }
 
 __global__ void finalize_kernel(int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
-                                int* pos_dev, int* step_dev) {
+                                int* pos_dev, int* step_dev, unsigned* epoch) {
   const int b = threadIdx.x;
   const int step = *step_dev;
   __syncthreads();
@@ -385,12 +385,13 @@ __global__ void finalize_kernel(int B, unsigned long long* keys, uint32_t* token
   if (b == 0) {
     *pos_dev += 1;
     *step_dev = step + 1;
+    if (epoch) *epoch += 1u;
   }
 }
 
 void launch_finalize(hipStream_t s, int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
-                     int* pos_dev, int* step_dev) {
-  finalize_kernel<<<1, 64, 0, s>>>(B, keys, token, ids_out, ld_ids, pos_dev, step_dev);
+                     int* pos_dev, int* step_dev, unsigned* epoch) {
+  finalize_kernel<<<1, 64, 0, s>>>(B, keys, token, ids_out, ld_ids, pos_dev, step_dev, epoch);
 }
 
 __global__ void keys_to_tokens_kernel(int B, unsigned long long* keys, uint32_t* token) {

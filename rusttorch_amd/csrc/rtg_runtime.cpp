@@ -162,6 +162,8 @@ static void ensure_rows(rtg_cache* c, size_t rows) {
 static void ensure_logits(rtg_cache* c, size_t rows) {
   if (rows <= c->logit_rows_cap) return;
   destroy_graph(c);
+  if (c->pstate) persistent_state_destroy(c->pstate);  // it holds the logits pointer
+  c->pstate = nullptr;
   if (c->logits) hipFree(c->logits);
   c->logits = nullptr;
   size_t cap = std::max<size_t>(rows, 16);
@@ -259,7 +261,7 @@ static void enqueue_decode_step(rtg_cache* c) {
   hipStream_t s = c->stream;
   const int P = (int)m->cfg.n_positions;
   if (c->pstate) {
-    persistent_decode_step(c->pstate, s);
+    HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/false));
   } else {
     launch_embed(s, m->wte, m->wtype, m->wpe, c->token_dev, B, 1, 0, c->pos_dev, d, c->x);
     for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -277,7 +279,8 @@ static void enqueue_decode_step(rtg_cache* c) {
     launch_gemv(s, B, m->wte, m->wtype, nullptr, c->ln, d, c->logits, V, V, d, EPI_NONE);
     launch_argmax(s, c->logits, V, B, V, c->keys);
   }
-  launch_finalize(s, B, c->keys, c->token_dev, c->ids_dev, P, c->pos_dev, c->step_dev);
+  launch_finalize(s, B, c->keys, c->token_dev, c->ids_dev, P, c->pos_dev, c->step_dev,
+                  c->pstate ? persistent_epoch(c->pstate) : nullptr);
 }
 
 static void set_counters(rtg_cache* c, int pos, int step) {
@@ -369,7 +372,10 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   ensure_rows(c, B * n);
   ensure_logits(c, B * n);
   hipStream_t s = c->stream;
-  if (!c->pstate && persistent_supported(m->pplan, (int)B)) c->pstate = persistent_state_create(m->pplan, c->k, c->v, (int)B, c->token_dev, c->pos_dev, c->logits, c->keys);
+  if (!c->pstate && persistent_supported(m->pplan, (int)B)) {
+    c->pstate = persistent_state_create(m->pplan, c->k, c->v, (int)B, c->token_dev, c->pos_dev, c->logits, c->keys);
+    destroy_graph(c);  // the step graph changes shape
+  }
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
   HIPX(hipEventRecord(c->ev[0], s));
   enqueue_prefill(c, c->ids_in, B, n, 0, 0);
@@ -383,9 +389,43 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   ensure_graph(c);
   for (size_t i = 1; i < steps; ++i) HIPX(hipGraphLaunch(c->graph_exec, s));
   HIPX(hipEventRecord(c->ev[2], s));
+  // Optional profiling pass: rewind to the first decode step and replay the
+  // steps launch by launch with events around the persistent kernel. Inputs
+  // (tokens, positions, cache rows) are the same, so are the results.
+  double kern_ms = 0.0;
+  size_t kern_n = 0;
+  if (timing && timing->profile_kernels && c->pstate && steps > 1) {
+    std::vector<hipEvent_t> evs(2 * (steps - 1));
+    for (auto& e : evs) HIPX(hipEventCreate(&e));
+    set_counters(c, (int)n, 1);
+    HIPX(hipMemcpyAsync(c->token_dev, c->ids_dev, 4, hipMemcpyDeviceToDevice, s));
+    for (size_t i = 1; i < steps; ++i) {
+      HIPX(hipEventRecord(evs[2 * (i - 1)], s));
+      HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/true));
+      HIPX(hipEventRecord(evs[2 * (i - 1) + 1], s));
+      launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev,
+                      persistent_epoch(c->pstate));
+    }
+    HIPX(hipStreamSynchronize(s));
+    for (size_t i = 0; i + 1 < evs.size(); i += 2) {
+      float ms = 0.f;
+      HIPX(hipEventElapsedTime(&ms, evs[i], evs[i + 1]));
+      kern_ms += ms;
+      ++kern_n;
+    }
+    for (auto& e : evs) hipEventDestroy(e);
+  }
   std::vector<uint32_t> gen(B * P);
   HIPX(hipMemcpyAsync(gen.data(), c->ids_dev, B * P * 4, hipMemcpyDeviceToHost, s));
   HIPX(hipStreamSynchronize(s));
+  if (c->pstate) {
+    unsigned e = 0;
+    HIPX(hipMemcpy(&e, persistent_err(c->pstate), 4, hipMemcpyDeviceToHost));
+    if (e) {
+      HIPX(hipMemset(persistent_err(c->pstate), 0, 4));
+      throw HipError{fmt("persistent decode step timed out waiting for a peer (code %u)", e)};
+    }
+  }
   c->len = n + steps - 1;  // the last generated token is never fed back
   const size_t outlen = n + steps;
   for (size_t b = 0; b < B; ++b) {
@@ -399,8 +439,8 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
     timing->prefill_ms = a;
     timing->decode_ms = b2;
     timing->decode_steps = steps - 1;
-    timing->decode_step_kernel_ms = 0.0;
-    timing->decode_step_kernel_launches = 0;
+    timing->decode_kernel_ms = kern_ms;
+    timing->decode_kernel_launches = kern_n;
   }
 }
 

@@ -234,17 +234,23 @@ class Gpt2Model:
         check(self._lib.rtg_generate_with_config(self._h, _ptr(ids), ids.size, C.byref(gc), _ptr(out)))
         return out.tolist()
 
-    def generate_cached_batched(self, prompts, max_new_tokens: int, timing: bool = False):
-        """Batched greedy generate_cached: prompts [B, n] -> ids [B, n + max(1, max_new)]."""
+    def generate_cached_batched(self, prompts, max_new_tokens: int, timing: bool = False,
+                                profile_kernels: bool = False):
+        """Batched greedy generate_cached: prompts [B, n] -> ids [B, n + max(1, max_new)].
+
+        timing=True also returns the device-event timings; profile_kernels=True
+        additionally replays the decode steps launch by launch to time the
+        decode-step kernel itself."""
         ids = np.atleast_2d(_ids(prompts))
         B, n = ids.shape
         ids = np.ascontiguousarray(ids)
         out = np.empty((B, n + max(1, max_new_tokens)), dtype=np.uint32)
         t = _lib.Timing()
+        t.profile_kernels = int(profile_kernels)
         check(self._lib.rtg_generate_cached_batched(self._h, _ptr(ids), B, n, max_new_tokens, _ptr(out),
                                                     C.byref(t)))
         if timing:
             return out, {"prefill_ms": t.prefill_ms, "decode_ms": t.decode_ms, "decode_steps": t.decode_steps,
-                         "decode_step_kernel_ms": t.decode_step_kernel_ms,
-                         "decode_step_kernel_launches": t.decode_step_kernel_launches}
+                         "decode_kernel_ms": t.decode_kernel_ms,
+                         "decode_kernel_launches": t.decode_kernel_launches}
         return out
