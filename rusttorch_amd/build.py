@@ -23,7 +23,9 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", f"-I{os.path.join(PKG, '..', 'include')}"]
 
-SOURCES = ["kernels.hip", "decode_persistent.hip", "rtg_runtime.cpp", "safetensors_reader.cpp"]
+SOURCES = ["kernels.hip", "decode_persistent.hip", "decode_persistent_inst_mini.hip",
+           "decode_persistent_inst_small.hip", "decode_persistent_inst_medium.hip",
+           "decode_persistent_inst_large.hip", "rtg_runtime.cpp", "safetensors_reader.cpp"]
 
 
 def _compile(src: str) -> str:

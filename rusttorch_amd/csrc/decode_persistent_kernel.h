@@ -1,0 +1,684 @@
+// Device side of the persistent decode step (batch 1), templated on the model
+// width D, vocabulary V and weight storage WT so that every segment count and
+// row split is a compile-time constant. Included by the per-size
+// instantiation files; see decode_persistent.hip for the host side.
+//
+// One cooperative launch runs a whole forward_cached(&[token]) + argmax
+// (rusttorch-core/src/nn/gpt2.rs:358-399, 858-868) on all 256 CUs:
+//  * Every weight matrix is streamed once per step. Workgroup w owns the
+//    output rows [w*RPW, (w+1)*RPW) of every phase; its GEMV waves hold their
+//    share of a phase's weights in registers, loaded one phase ahead into two
+//    alternating buffers, so HBM keeps streaming while workgroups exchange
+//    activations.
+//  * Workgroups exchange activations without grid barriers or agent-scope
+//    fences (~1-2 us each on this part): each published value is a 64-bit
+//    word {tag, f32} written with one relaxed agent-scope atomic store, and
+//    readers poll until every tag equals the step's epoch. Each (layer, phase)
+//    has its own buffer, so a word is written once per step and never
+//    overwritten while someone may still read it.
+//  * Waves are specialised so that no wave holding in-flight weight loads
+//    ever has to drain them for a publication:
+//      wave 0         leader: LayerNorm, attention merge, epilogues, stores
+//      waves 1..NA    helpers: poll inputs with the leader; attention
+//      waves NA+1..   GEMV waves: weights in registers, dot products
+//    Leader/helpers and GEMV waves meet only through LDS counters, and all
+//    pointers are address-space qualified so no flat access ties the LDS
+//    counter (lgkmcnt) to global loads.
+//  * Every wait is bounded; a timeout sets *err and lets the step finish with
+//    wrong numbers instead of hanging; the host turns *err into an error.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+namespace rtg {
+namespace pk {
+
+constexpr int G = 256;              // workgroups = CUs of an MI355X
+// 8 waves per workgroup = 2 per SIMD, which leaves 256 VGPRs per wave for the
+// two register-resident weight buffers.
+constexpr int NA = 2;               // helper waves
+constexpr int NC = 5;               // GEMV waves
+constexpr int NGLUE = 1 + NA;       // leader + helpers
+constexpr int NTHREADS = (1 + NA + NC) * 64;
+constexpr int HD = 64;              // head_dim of every GPT-2 size
+constexpr int CMAX = 16;            // attention chunks per head
+constexpr int ITEM_WORDS = 2 + HD;  // m, l, o[64]
+constexpr int MAX_ITEMS = 64;       // heads * chunks merged by the consumers
+constexpr int MAXW = 12;            // polled words per glue lane per round
+constexpr int PART_MAX = 1536;      // segment partials per workgroup
+constexpr int ATT_POS_MAX = 256;    // positions per helper wave per item
+constexpr unsigned SPIN_CAP = 1u << 21;
+
+typedef unsigned long long u64;
+
+#define PK_G(T, p) ((const __attribute__((address_space(1))) T*)(p))
+#define PK_GW(T, p) ((__attribute__((address_space(1))) T*)(p))
+
+struct LayerPtrs {
+  const void *wqkv, *waproj, *wfc, *wmproj;
+  const float *bqkv, *baproj, *bfc, *bmproj, *ln1w, *ln1b, *ln2w, *ln2b;
+};
+
+struct Params {
+  const LayerPtrs* layers;
+  const void* wte;
+  const float *wpe, *lnfw, *lnfb;
+  int L, P;
+  float eps;
+  float* kc;  // [L][H][P][HD]
+  float* vc;
+  long kv_layer;  // floats per layer
+  const uint32_t* token;
+  const int* pos;
+  const unsigned* epoch;
+  u64* tag;  // tagged words, lw per layer
+  long lw;
+  int o_qkv, o_att, o_x2, o_h, o_x3;
+  float* logits;
+  u64* keys;
+  unsigned* err;
+};
+
+// Row split of one GEMV phase: N outputs, each a dot product over K inputs
+// stored as VR 16-byte vectors; a segment = 64 vectors of one row.
+template <int N_, int K_, int E_, int SPW_ = 0>
+struct Geom {
+  static constexpr int N = N_, K = K_, VR = K_ / E_, SPR = (VR + 63) / 64;
+  static constexpr int RPW = (N_ + G - 1) / G;
+  static constexpr int SEGS = RPW * SPR;
+  static constexpr int SPW = SPW_ ? SPW_ : (SEGS + NC - 1) / NC;
+};
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+template <int D_, int V_, int WT_>
+struct Cfg {
+  static constexpr int D = D_, V = V_, WT = WT_, H = D_ / HD, E = WT_ == W_BF16 ? 8 : 4;
+  typedef Geom<3 * D, D, E> GQ;
+  typedef Geom<D, D, E> GP;
+  typedef Geom<4 * D, D, E> GF;
+  typedef Geom<D, 4 * D, E> GM;
+  static constexpr int MAXSEG = cmax(cmax(GQ::SPW, GP::SPW), cmax(GF::SPW, GM::SPW));
+  typedef Geom<V, D, E, MAXSEG> GL;  // LM head, streamed in chunks of MAXSEG per wave
+  static_assert(D % HD == 0 && D <= 1600, "model width");
+  static_assert(GQ::SEGS <= PART_MAX && GF::SEGS <= PART_MAX && GM::SEGS <= PART_MAX && GL::SEGS <= PART_MAX,
+                "segment partials exceed LDS");
+  static_assert(H <= MAX_ITEMS, "heads");
+};
+
+template <int D>
+struct Smem {
+  float in_vec[2][4 * D];  // GEMV input, double-buffered by phase parity
+  float xraw[D];           // residual input of the current layer
+  float x2raw[D];          // residual after attention
+  float part[PART_MAX];
+  float stage[MAX_ITEMS * ITEM_WORDS];
+  float att_q[HD], att_k[HD], att_v[HD];
+  float att_s[NA][ATT_POS_MAX];
+  float att_part[NA][ITEM_WORDS];
+  unsigned gemv_ready, gemv_done, glue_cnt;
+};
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ u64 tload(const u64* p) {
+  return __hip_atomic_load(PK_GW(u64, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tstore(u64* p, float v, unsigned tag) {
+  __hip_atomic_store(PK_GW(u64, p), ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+// Native vector types for address-space qualified loads (HIP's float4 class
+// does not copy from an address-space qualified object).
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld4g(const float* p) {
+  const f4v v = PK_G(f4v, p)[0];
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ unsigned lds_load(unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_add(unsigned* p, unsigned v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Order this wave's LDS accesses (lgkmcnt only).
+__device__ __forceinline__ void lds_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local"); }
+__device__ __forceinline__ void lds_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local"); }
+
+__device__ __forceinline__ bool err_set(const unsigned* err) {
+  return __hip_atomic_load(PK_GW(unsigned, err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+__device__ __forceinline__ void raise_err(unsigned* err, unsigned code) {
+  __hip_atomic_fetch_or(PK_GW(unsigned, err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Spin (whole wave) until *p >= target (LDS counter). Bounded.
+__device__ __forceinline__ void lds_wait_ge(unsigned* p, unsigned target, unsigned* err) {
+  unsigned spins = 0;
+  while (lds_load(p) < target) {
+    __builtin_amdgcn_s_sleep(1);
+    if (++spins > (SPIN_CAP << 3)) {
+      raise_err(err, 2u);
+      break;
+    }
+  }
+  lds_acquire();
+}
+
+__device__ __forceinline__ float wsum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wmax(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// gelu_new, gpt2.rs:837-847 (the reference's association).
+__device__ __forceinline__ float gelu_new(float x) {
+  const float sqrt_2_pi = 0.7978845608028654f;
+  float inner = sqrt_2_pi * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+template <int WT>
+struct V16;
+template <>
+struct V16<W_F32> {
+  typedef f4v T;
+  static constexpr int E = 4;
+  __device__ __forceinline__ static float dot(const T& w, const float* x) {
+    const float4 xv = *reinterpret_cast<const float4*>(x);
+    return w.x * xv.x + w.y * xv.y + w.z * xv.z + w.w * xv.w;
+  }
+};
+template <>
+struct V16<W_BF16> {
+  typedef u4v T;
+  static constexpr int E = 8;
+  // bf16_to_f32 = bits << 16 (nn/safetensors.rs:389-391)
+  __device__ __forceinline__ static float dot(const T& w, const float* x) {
+    const float4 a = *reinterpret_cast<const float4*>(x);
+    const float4 c = *reinterpret_cast<const float4*>(x + 4);
+    float s = __uint_as_float(w.x << 16) * a.x + __uint_as_float(w.x & 0xffff0000u) * a.y;
+    s += __uint_as_float(w.y << 16) * a.z + __uint_as_float(w.y & 0xffff0000u) * a.w;
+    s += __uint_as_float(w.z << 16) * c.x + __uint_as_float(w.z & 0xffff0000u) * c.y;
+    s += __uint_as_float(w.w << 16) * c.z + __uint_as_float(w.w & 0xffff0000u) * c.w;
+    return s;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// GEMV waves. Wave cw of workgroup wg handles workgroup segments
+// [seg_base + cw*SPW, seg_base + (cw+1)*SPW). All bookkeeping is scalar.
+// ---------------------------------------------------------------------------
+
+template <int WT, int MAXSEG, class GEO>
+__device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], const void* W, int wg, int cw, int lane,
+                                          int seg_base) {
+  typedef typename V16<WT>::T Vec;
+  const int row0 = wg * GEO::RPW;
+  const int rows_here = min(GEO::RPW, GEO::N - row0);
+  const int segs_here = rows_here > 0 ? rows_here * GEO::SPR : 0;
+  const int s0 = seg_base + cw * GEO::SPW;
+  const int nseg = min(GEO::SPW, segs_here - s0);
+  int lr = s0 / GEO::SPR, j = s0 - lr * GEO::SPR;
+  const Vec* base = reinterpret_cast<const Vec*>(W) + (long)row0 * GEO::VR;
+#pragma unroll
+  for (int i = 0; i < MAXSEG; ++i) {
+    if (i < GEO::SPW && i < nseg) {
+      const Vec* rowp = base + (long)lr * GEO::VR + j * 64;
+      if (GEO::VR % 64 == 0 || j * 64 + 64 <= GEO::VR) buf[i] = PK_G(Vec, rowp)[lane];
+      else buf[i] = PK_G(Vec, rowp)[min(lane, GEO::VR - j * 64 - 1)];
+    }
+    if (++j == GEO::SPR) {
+      j = 0;
+      ++lr;
+    }
+  }
+}
+
+template <int WT, int MAXSEG, class GEO>
+__device__ __forceinline__ void seg_compute(const typename V16<WT>::T (&buf)[MAXSEG], const float* x, float* part,
+                                            int wg, int cw, int lane, int seg_base) {
+  constexpr int E = V16<WT>::E;
+  const int row0 = wg * GEO::RPW;
+  const int rows_here = min(GEO::RPW, GEO::N - row0);
+  const int segs_here = rows_here > 0 ? rows_here * GEO::SPR : 0;
+  const int s0 = seg_base + cw * GEO::SPW;
+  const int nseg = min(GEO::SPW, segs_here - s0);
+  int j = s0 % GEO::SPR;
+#pragma unroll
+  for (int i = 0; i < MAXSEG; ++i) {
+    if (i < GEO::SPW && i < nseg) {
+      const int v = j * 64 + lane;
+      const float d = V16<WT>::dot(buf[i], x + min(v, GEO::VR - 1) * E);
+      const float acc = wsum(v < GEO::VR ? d : 0.f);
+      if (lane == 0) part[s0 + i] = acc;
+    }
+    if (++j == GEO::SPR) j = 0;
+  }
+}
+
+template <class C>
+__device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int cw, int lane) {
+  constexpr int WT = C::WT, MS = C::MAXSEG;
+  typedef typename V16<WT>::T Vec;
+  typedef typename C::GQ GQ;
+  typedef typename C::GP GP;
+  typedef typename C::GF GF;
+  typedef typename C::GM GM;
+  typedef typename C::GL GL;
+  const int wg = blockIdx.x;
+  Vec A[MS], B[MS];
+  unsigned seq = 0;
+  const LayerPtrs* LP = p.layers;
+  seg_issue<WT, MS, GQ>(A, LP[0].wqkv, wg, cw, lane, 0);
+  seg_issue<WT, MS, GP>(B, LP[0].waproj, wg, cw, lane, 0);
+  for (int l = 0; l < p.L; ++l) {
+    const bool last = l + 1 == p.L;
+    // QKV from A; refill A with this layer's FC weights
+    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
+    seg_compute<WT, MS, GQ>(A, sm.in_vec[1], sm.part, wg, cw, lane, 0);
+    lds_release();
+    if (lane == 0) lds_add(&sm.gemv_done, 1);
+    seg_issue<WT, MS, GF>(A, LP[l].wfc, wg, cw, lane, 0);
+    // attention projection from B; refill B with the MLP projection
+    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
+    seg_compute<WT, MS, GP>(B, sm.in_vec[0], sm.part, wg, cw, lane, 0);
+    lds_release();
+    if (lane == 0) lds_add(&sm.gemv_done, 1);
+    seg_issue<WT, MS, GM>(B, LP[l].wmproj, wg, cw, lane, 0);
+    // FC from A; refill A with the next layer's QKV (or the LM head's chunk 0)
+    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
+    seg_compute<WT, MS, GF>(A, sm.in_vec[1], sm.part, wg, cw, lane, 0);
+    lds_release();
+    if (lane == 0) lds_add(&sm.gemv_done, 1);
+    if (!last) seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, wg, cw, lane, 0);
+    else seg_issue<WT, MS, GL>(A, p.wte, wg, cw, lane, 0);
+    // MLP projection from B; refill B with the next layer's attention projection (or LM chunk 1)
+    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
+    seg_compute<WT, MS, GM>(B, sm.in_vec[0], sm.part, wg, cw, lane, 0);
+    lds_release();
+    if (lane == 0) lds_add(&sm.gemv_done, 1);
+    if (!last) seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, wg, cw, lane, 0);
+    else seg_issue<WT, MS, GL>(B, p.wte, wg, cw, lane, NC * GL::SPW);
+  }
+  // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
+  // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
+  lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
+  constexpr int PER_CHUNK = NC * GL::SPW;
+  const int rows_here = min(GL::RPW, GL::N - wg * GL::RPW);
+  const int segs_here = rows_here > 0 ? rows_here * GL::SPR : 0;
+  for (int base = 0; base < segs_here; base += 2 * PER_CHUNK) {
+    seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base);
+    if (base + 2 * PER_CHUNK < segs_here) seg_issue<WT, MS, GL>(A, p.wte, wg, cw, lane, base + 2 * PER_CHUNK);
+    if (base + PER_CHUNK < segs_here) {
+      seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK);
+      if (base + 3 * PER_CHUNK < segs_here) seg_issue<WT, MS, GL>(B, p.wte, wg, cw, lane, base + 3 * PER_CHUNK);
+    }
+  }
+  lds_release();
+  if (lane == 0) lds_add(&sm.gemv_done, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Leader + helper waves ("glue").
+// ---------------------------------------------------------------------------
+
+template <int D>
+__device__ __forceinline__ void glue_barrier(Smem<D>& sm, unsigned& gen, int lane, unsigned* err) {
+  ++gen;
+  lds_release();
+  if (lane == 0) lds_add(&sm.glue_cnt, 1);
+  lds_wait_ge(&sm.glue_cnt, gen * NGLUE, err);
+}
+
+// All glue lanes poll n tagged words into dst, MAXW words per lane per round
+// (all loads of a round in flight together).
+__device__ __forceinline__ void glue_poll(const u64* src, int n, unsigned tag, float* dst, int gl, unsigned* err) {
+  constexpr int NG = NGLUE * 64;
+  const bool skip = err_set(err);
+  for (int base = 0; base < n; base += MAXW * NG) {
+    u64 w[MAXW];
+#pragma unroll
+    for (int k = 0; k < MAXW; ++k) {
+      const int i = base + gl + k * NG;
+      w[k] = (i < n && !skip) ? tload(src + i) : ((u64)tag << 32);
+    }
+    unsigned spins = 0;
+    for (;;) {
+      bool all = true;
+#pragma unroll
+      for (int k = 0; k < MAXW; ++k)
+        if ((unsigned)(w[k] >> 32) != tag) all = false;
+      if (all) break;
+      if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(err))) {
+        raise_err(err, 1u);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int k = 0; k < MAXW; ++k) {
+        const int i = base + gl + k * NG;
+        if (i < n && (unsigned)(w[k] >> 32) != tag) w[k] = tload(src + i);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < MAXW; ++k) {
+      const int i = base + gl + k * NG;
+      if (i < n) dst[i] = __uint_as_float((unsigned)w[k]);
+    }
+  }
+}
+
+// Leader only: LayerNorm of src[D] into dst (gpt2.rs:636-666, two-pass).
+template <int D>
+__device__ __forceinline__ void leader_layernorm(const float* src, const float* w, const float* b, float eps,
+                                                 float* dst, int lane) {
+  float s = 0.f;
+  for (int i = lane; i < D; i += 64) s += src[i];
+  const float mean = wsum(s) / (float)D;
+  float v = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    const float t = src[i] - mean;
+    v += t * t;
+  }
+  const float var = wsum(v) / (float)D;
+  const float inv_std = 1.0f / sqrtf(var + eps);
+  for (int i = lane; i < D; i += 64) dst[i] = (src[i] - mean) * inv_std * PK_G(float, w)[i] + PK_G(float, b)[i];
+}
+
+// Leader only: publish in_vec to the GEMV waves and wait for their partials.
+template <int D>
+__device__ __forceinline__ void leader_run_gemv(Smem<D>& sm, unsigned& seq, int lane, unsigned* err) {
+  lds_release();
+  ++seq;
+  if (lane == 0) __hip_atomic_store(&sm.gemv_ready, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  lds_wait_ge(&sm.gemv_done, seq * NC, err);
+}
+
+// Row sums acc(lr) = sum_j part[lr*SPR + j] (ascending j).
+template <class GEO, int D>
+__device__ __forceinline__ float row_acc(const Smem<D>& sm, int lr) {
+  float a = 0.f;
+#pragma unroll
+  for (int j = 0; j < GEO::SPR; ++j) a += sm.part[lr * GEO::SPR + j];
+  return a;
+}
+
+template <class C>
+__device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int gw, int lane, int len, int NCH,
+                                          int items, unsigned tag) {
+  constexpr int D = C::D, H = C::H;
+  typedef typename C::GQ GQ;
+  typedef typename C::GP GP;
+  typedef typename C::GF GF;
+  typedef typename C::GM GM;
+  typedef typename C::GL GL;
+  const bool leader = gw == 0;
+  const int gl = gw * 64 + lane;
+  const int wg = blockIdx.x;
+  unsigned gen = 0, seq = 0;
+  const int pos = len - 1;
+  // embedding (gpt2.rs:377-384): every workgroup computes x0 itself
+  if (leader) {
+    const uint32_t tok = *PK_G(uint32_t, p.token);
+    for (int i = lane; i < D; i += 64) {
+      float w;
+      if (C::WT == W_F32) w = PK_G(float, p.wte)[(long)tok * D + i];
+      else w = __uint_as_float((uint32_t)PK_G(uint16_t, p.wte)[(long)tok * D + i] << 16);
+      sm.xraw[i] = w + PK_G(float, p.wpe)[(long)pos * D + i];
+    }
+  }
+  const int item = wg < items ? wg : -1;
+  const int ih = item >= 0 ? item / NCH : 0, ic = item >= 0 ? item - ih * NCH : 0;
+  const int CL = (len + NCH - 1) / NCH;
+  const int j0 = ic * CL, j1 = min(len, j0 + CL);
+  for (int l = 0; l < p.L; ++l) {
+    const LayerPtrs& LP = p.layers[l];
+    u64* T = p.tag + (long)l * p.lw;
+    // ---- QKV: LN1(x) @ c_attn + bias; k/v of the new token into the cache ----
+    if (l > 0) {
+      glue_poll(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
+      glue_barrier(sm, gen, lane, p.err);
+    }
+    if (leader) {
+      leader_layernorm<D>(sm.xraw, LP.ln1w, LP.ln1b, p.eps, sm.in_vec[1], lane);
+      leader_run_gemv(sm, seq, lane, p.err);
+      const int row0 = wg * GQ::RPW, rows_here = min(GQ::RPW, GQ::N - row0);
+      float* kl = p.kc + (long)l * p.kv_layer;
+      float* vl = p.vc + (long)l * p.kv_layer;
+      for (int lr = lane; lr < rows_here; lr += 64) {
+        const int n = row0 + lr;
+        const float v = row_acc<GQ>(sm, lr) + PK_G(float, LP.bqkv)[n];
+        tstore(T + p.o_qkv + n, v, tag);
+        if (n >= D) {
+          const int c = n < 2 * D ? n - D : n - 2 * D;
+          const int h = c / HD, dd = c - h * HD;
+          float* base = n < 2 * D ? kl : vl;
+          PK_GW(float, base)[((long)h * p.P + pos) * HD + dd] = v;
+        }
+      }
+    }
+    // ---- attention (multi_head_attention_cached, gpt2.rs:772-834): one item
+    //      per workgroup = head ih, positions [j0, j1) ----
+    if (item >= 0) {
+      if (leader) {
+        float* dsts[3] = {sm.att_q, sm.att_k, sm.att_v};
+        for (int part = 0; part < 3; ++part) {
+          const u64* src = T + p.o_qkv + part * D + ih * HD;
+          u64 w = tload(src + lane);
+          unsigned spins = 0;
+          while ((unsigned)(w >> 32) != tag) {
+            if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(p.err))) {
+              raise_err(p.err, 1u);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            w = tload(src + lane);
+          }
+          dsts[part][lane] = __uint_as_float((unsigned)w);
+        }
+      }
+      glue_barrier(sm, gen, lane, p.err);
+      if (!leader) {
+        const int hw = gw - 1;
+        const int per = (j1 - j0 + NA - 1) / NA;
+        const int a0 = j0 + hw * per, a1 = min(j1, a0 + per);
+        const float* Kh = p.kc + (long)l * p.kv_layer + (long)ih * p.P * HD;
+        const float* Vh = p.vc + (long)l * p.kv_layer + (long)ih * p.P * HD;
+        const int grp = lane >> 4, dq = (lane & 15) * 4;
+        const float scale = 0.125f;  // 1 / sqrt(64)
+        const float4 q4 = *reinterpret_cast<const float4*>(sm.att_q + dq);
+        float mloc = -INFINITY;
+        for (int jb = a0; jb < a1; jb += 4) {  // 4 positions per iteration, 16 lanes each
+          const int j = jb + grp;
+          float dot = 0.f;
+          if (j < a1) {
+            const float4 k4 = j == pos ? *reinterpret_cast<const float4*>(sm.att_k + dq)
+                                       : ld4g(Kh + (long)j * HD + dq);
+            dot = q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+          }
+#pragma unroll
+          for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+          float s = -INFINITY;
+          if (j < a1) {
+            s = dot * scale;
+            if ((lane & 15) == 0) sm.att_s[hw][j - a0] = s;
+          }
+          mloc = fmaxf(mloc, s);
+        }
+        const float m = wmax(mloc);
+        lds_release();
+        lds_acquire();
+        float lsum = 0.f;
+        float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int jb = a0; jb < a1; jb += 4) {
+          const int j = jb + grp;
+          if (j >= a1) continue;
+          const float pj = expf(sm.att_s[hw][j - a0] - m);
+          const float4 v4 = j == pos ? *reinterpret_cast<const float4*>(sm.att_v + dq)
+                                     : ld4g(Vh + (long)j * HD + dq);
+          if ((lane & 15) == 0) lsum += pj;
+          o4.x += pj * v4.x;
+          o4.y += pj * v4.y;
+          o4.z += pj * v4.z;
+          o4.w += pj * v4.w;
+        }
+        lsum = wsum(lsum);
+#pragma unroll
+        for (int o = 16; o < 64; o <<= 1) {
+          o4.x += __shfl_xor(o4.x, o, 64);
+          o4.y += __shfl_xor(o4.y, o, 64);
+          o4.z += __shfl_xor(o4.z, o, 64);
+          o4.w += __shfl_xor(o4.w, o, 64);
+        }
+        if (lane < 16) {
+          sm.att_part[hw][2 + dq + 0] = o4.x;
+          sm.att_part[hw][2 + dq + 1] = o4.y;
+          sm.att_part[hw][2 + dq + 2] = o4.z;
+          sm.att_part[hw][2 + dq + 3] = o4.w;
+        }
+        if (lane == 0) {
+          sm.att_part[hw][0] = a1 > a0 ? m : -INFINITY;
+          sm.att_part[hw][1] = a1 > a0 ? lsum : 0.f;
+        }
+      }
+      glue_barrier(sm, gen, lane, p.err);
+      if (leader) {  // merge the helpers' (m, l, o) into the item's partial softmax
+        float M = -INFINITY;
+        for (int w = 0; w < NA; ++w) M = fmaxf(M, sm.att_part[w][0]);
+        float Ls = 0.f, o = 0.f;
+        for (int w = 0; w < NA; ++w) {
+          const float mw = sm.att_part[w][0];
+          if (mw == -INFINITY) continue;
+          const float f = expf(mw - M);
+          Ls += sm.att_part[w][1] * f;
+          o += sm.att_part[w][2 + lane] * f;
+        }
+        u64* dst = T + p.o_att + (long)item * ITEM_WORDS;
+        tstore(dst + 2 + lane, o, tag);
+        if (lane == 0) {
+          tstore(dst, M, tag);
+          tstore(dst + 1, Ls, tag);
+        }
+      }
+    }
+    // ---- attention projection + residual (gpt2.rs:523-526) ----
+    glue_poll(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
+    glue_barrier(sm, gen, lane, p.err);
+    if (leader) {
+      for (int h = 0; h < H; ++h) {  // merge the chunks of each head
+        float M = -INFINITY;
+        for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS]);
+        float Ls = 0.f, o = 0.f;
+        for (int c = 0; c < NCH; ++c) {
+          const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
+          if (it[0] == -INFINITY) continue;
+          const float f = expf(it[0] - M);
+          Ls += it[1] * f;
+          o += it[2 + lane] * f;
+        }
+        sm.in_vec[0][h * HD + lane] = o / Ls;
+      }
+      leader_run_gemv(sm, seq, lane, p.err);
+      const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
+      for (int lr = lane; lr < rows_here; lr += 64) {
+        const int n = row0 + lr;
+        tstore(T + p.o_x2 + n, sm.xraw[n] + (row_acc<GP>(sm, lr) + PK_G(float, LP.baproj)[n]), tag);
+      }
+    }
+    // ---- FC + gelu_new (gpt2.rs:529-533) ----
+    glue_poll(T + p.o_x2, D, tag, sm.x2raw, gl, p.err);
+    glue_barrier(sm, gen, lane, p.err);
+    if (leader) {
+      leader_layernorm<D>(sm.x2raw, LP.ln2w, LP.ln2b, p.eps, sm.in_vec[1], lane);
+      leader_run_gemv(sm, seq, lane, p.err);
+      const int row0 = wg * GF::RPW, rows_here = min(GF::RPW, GF::N - row0);
+      for (int lr = lane; lr < rows_here; lr += 64) {
+        const int n = row0 + lr;
+        tstore(T + p.o_h + n, gelu_new(row_acc<GF>(sm, lr) + PK_G(float, LP.bfc)[n]), tag);
+      }
+    }
+    // ---- MLP projection + residual (gpt2.rs:534-537) ----
+    glue_poll(T + p.o_h, 4 * D, tag, sm.in_vec[0], gl, p.err);
+    glue_barrier(sm, gen, lane, p.err);
+    if (leader) {
+      leader_run_gemv(sm, seq, lane, p.err);
+      const int row0 = wg * GM::RPW, rows_here = min(GM::RPW, GM::N - row0);
+      for (int lr = lane; lr < rows_here; lr += 64) {
+        const int n = row0 + lr;
+        tstore(T + p.o_x3 + n, sm.x2raw[n] + (row_acc<GM>(sm, lr) + PK_G(float, LP.bmproj)[n]), tag);
+      }
+    }
+  }
+  // ---- ln_f + tied LM head + argmax (gpt2.rs:392-396, 858-868) ----
+  glue_poll(p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
+  glue_barrier(sm, gen, lane, p.err);
+  if (leader) {
+    leader_layernorm<D>(sm.xraw, p.lnfw, p.lnfb, p.eps, sm.in_vec[1], lane);
+    leader_run_gemv(sm, seq, lane, p.err);
+    const int row0 = wg * GL::RPW, rows_here = min(GL::RPW, GL::N - row0);
+    u64 best = 0ull;
+    for (int lr = lane; lr < rows_here; lr += 64) {
+      const int n = row0 + lr;
+      const float v = row_acc<GL>(sm, lr);
+      PK_GW(float, p.logits)[n] = v;
+      u64 k = 0ull;
+      if (v > -INFINITY) {  // -inf and NaN never win (strict '>' from -inf)
+        uint32_t b = __float_as_uint(v);
+        b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+        k = ((u64)b << 32) | (u64)(~(uint32_t)n);
+      }
+      best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const u64 other = __shfl_xor(best, o, 64);
+      best = other > best ? other : best;
+    }
+    if (lane == 0 && best != 0ull)
+      __hip_atomic_fetch_max(PK_GW(u64, p.keys), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Attention chunking for this step: NCH chunks per head (>= 32 positions
+// each, at most CMAX and H*NCH <= min(MAX_ITEMS, G)).
+template <int H>
+__device__ __host__ __forceinline__ int att_chunks(int len) {
+  constexpr int cap0 = CMAX < MAX_ITEMS / H ? CMAX : MAX_ITEMS / H;
+  constexpr int cap = cap0 < G / H ? cap0 : G / H;
+  int c = (len + 31) / 32;
+  c = c < cap ? c : cap;
+  return c < 1 ? 1 : c;
+}
+
+template <int D, int V, int WT>
+__global__ __launch_bounds__(NTHREADS) void decode_step_kernel(Params p) {
+  typedef Cfg<D, V, WT> C;
+  __shared__ Smem<D> sm;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (threadIdx.x == 0) {
+    sm.gemv_ready = 0;
+    sm.gemv_done = 0;
+    sm.glue_cnt = 0;
+  }
+  __syncthreads();
+  const int len = *PK_G(int, p.pos) + 1;
+  const unsigned tag = *PK_G(unsigned, p.epoch);
+  const int nch = att_chunks<C::H>(len);
+  if (wave < NGLUE) glue_role<C>(p, sm, wave, lane, len, nch, C::H * nch, tag);
+  else gemv_role<C>(p, sm, wave - NGLUE, lane);
+}
+
+}  // namespace pk
+}  // namespace rtg
