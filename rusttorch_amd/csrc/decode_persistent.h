@@ -38,5 +38,7 @@ void persistent_state_destroy(PersistentState* s);
 hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative);
 unsigned* persistent_epoch(PersistentState* s);
 unsigned* persistent_err(PersistentState* s);
+// Writes the latest step's per-workgroup timestamps to $RTG_TRACE_FILE (if set).
+void persistent_dump_trace(PersistentState* s);
 
 }  // namespace rtg

@@ -3,6 +3,7 @@
 // (tagged exchange buffers, epoch, error flag) and the launch.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
 #include <stdlib.h>
 
 #include <vector>
@@ -42,6 +43,7 @@ struct PersistentPlan {
   const void* kernel = nullptr;  // null: shape not supported, the graph path runs
   pk::Params base{};
   pk::LayerPtrs* layers_dev = nullptr;
+  void* zeros = nullptr;
 };
 
 struct PersistentState {
@@ -50,6 +52,8 @@ struct PersistentState {
   pk::u64* tags = nullptr;
   unsigned* epoch = nullptr;
   unsigned* err = nullptr;
+  pk::u64* trace = nullptr;
+  unsigned* flags = nullptr;
 };
 
 PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
@@ -82,7 +86,9 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   if (hipMalloc(&pl->layers_dev, sizeof(pk::LayerPtrs) * L) != hipSuccess) return pl;
   if (hipMemcpy(pl->layers_dev, lp.data(), sizeof(pk::LayerPtrs) * L, hipMemcpyHostToDevice) != hipSuccess)
     return pl;
+  if (hipMalloc(&pl->zeros, 4096) != hipSuccess || hipMemset(pl->zeros, 0, 4096) != hipSuccess) return pl;
   pk::Params& p = pl->base;
+  p.dummy = pl->zeros;
   p.layers = pl->layers_dev;
   p.wte = w.wte;
   p.wpe = w.wpe;
@@ -106,6 +112,7 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
 void persistent_plan_destroy(PersistentPlan* pl) {
   if (!pl) return;
   if (pl->layers_dev) hipFree(pl->layers_dev);
+  if (pl->zeros) hipFree(pl->zeros);
   delete pl;
 }
 
@@ -124,13 +131,15 @@ PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, floa
   s->p = pl->base;
   pk::Params& p = s->p;
   const size_t words = (size_t)p.lw * p.L;
+  const size_t nflags = (size_t)pk::F_LAYER * p.L;
   if (hipMalloc(&s->tags, words * 8) != hipSuccess || hipMalloc(&s->epoch, 256) != hipSuccess ||
-      hipMalloc(&s->err, 256) != hipSuccess) {
+      hipMalloc(&s->err, 256) != hipSuccess || hipMalloc(&s->flags, nflags * 4) != hipSuccess) {
     persistent_state_destroy(s);
     return nullptr;
   }
   // tag 0 never matches: the epoch starts at 1 and only grows
-  if (hipMemset(s->tags, 0, words * 8) != hipSuccess || hipMemset(s->err, 0, 256) != hipSuccess) {
+  if (hipMemset(s->tags, 0, words * 8) != hipSuccess || hipMemset(s->err, 0, 256) != hipSuccess ||
+      hipMemset(s->flags, 0, nflags * 4) != hipSuccess) {
     persistent_state_destroy(s);
     return nullptr;
   }
@@ -140,8 +149,17 @@ PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, floa
     return nullptr;
   }
   p.tag = s->tags;
+  p.flags = s->flags;
+  p.fl = pk::F_LAYER;
   p.epoch = s->epoch;
   p.err = s->err;
+  p.trace = nullptr;
+  if (const char* tf = getenv("RTG_TRACE_FILE")) {
+    // per-workgroup phase timestamps of the latest step, written on request
+    const size_t tbytes = (size_t)pk::G * pk::TRACE_STRIDE * 8;
+    if (tf[0] && hipMalloc(&s->trace, tbytes) == hipSuccess && hipMemset(s->trace, 0, tbytes) == hipSuccess)
+      p.trace = s->trace;
+  }
   p.kc = kcache;
   p.vc = vcache;
   p.token = token_dev;
@@ -156,7 +174,22 @@ void persistent_state_destroy(PersistentState* s) {
   if (s->tags) hipFree(s->tags);
   if (s->epoch) hipFree(s->epoch);
   if (s->err) hipFree(s->err);
+  if (s->trace) hipFree(s->trace);
+  if (s->flags) hipFree(s->flags);
   delete s;
+}
+
+void persistent_dump_trace(PersistentState* s) {
+  const char* tf = getenv("RTG_TRACE_FILE");
+  if (!s || !s->trace || !tf) return;
+  std::vector<pk::u64> h((size_t)pk::G * pk::TRACE_STRIDE);
+  if (hipMemcpy(h.data(), s->trace, h.size() * 8, hipMemcpyDeviceToHost) != hipSuccess) return;
+  if (FILE* f = fopen(tf, "wb")) {
+    const int hdr[4] = {pk::G, pk::TRACE_STRIDE, s->p.L, 0};
+    fwrite(hdr, sizeof hdr, 1, f);
+    fwrite(h.data(), 8, h.size(), f);
+    fclose(f);
+  }
 }
 
 unsigned* persistent_epoch(PersistentState* s) { return s ? s->epoch : nullptr; }

@@ -55,6 +55,7 @@ typedef unsigned long long u64;
 
 #define PK_G(T, p) ((const __attribute__((address_space(1))) T*)(p))
 #define PK_GW(T, p) ((__attribute__((address_space(1))) T*)(p))
+#define PK_C(T, p) ((const __attribute__((address_space(4))) T*)(p))
 
 struct LayerPtrs {
   const void *wqkv, *waproj, *wfc, *wmproj;
@@ -76,10 +77,25 @@ struct Params {
   u64* tag;  // tagged words, lw per layer
   long lw;
   int o_qkv, o_att, o_x2, o_h, o_x3;
+  unsigned* flags;  // producer flags, fl per layer: x2[G], h[G], x3[G], att[MAX_ITEMS]
+  long fl;
   float* logits;
   u64* keys;
   unsigned* err;
+  u64* trace;         // optional: per-workgroup timestamps (TRACE_STRIDE entries each)
+  const void* dummy;  // >= 1 KiB of zeros: target of the loads of segments a wave does not own
 };
+
+constexpr int TRACE_STRIDE = 2048;
+// flag array offsets within a layer's flags
+constexpr int F_X2 = 0, F_H = G, F_X3 = 2 * G, F_ATT = 3 * G, F_LAYER = 3 * G + MAX_ITEMS;
+
+// Timestamp (100 MHz constant clock) of a trace point, written by lane 0.
+#define PK_TRACE(p, idx, lane)                                                                 \
+  do {                                                                                         \
+    if ((p).trace && (lane) == 0 && (idx) >= 0 && (idx) < TRACE_STRIDE)                                      \
+      PK_GW(u64, (p).trace)[(long)blockIdx.x * TRACE_STRIDE + (idx)] = wall_clock64();         \
+  } while (0)
 
 // Row split of one GEMV phase: N outputs, each a dot product over K inputs
 // stored as VR 16-byte vectors; a segment = 64 vectors of one row.
@@ -103,6 +119,7 @@ struct Cfg {
   static constexpr int MAXSEG = cmax(cmax(GQ::SPW, GP::SPW), cmax(GF::SPW, GM::SPW));
   typedef Geom<V, D, E, MAXSEG> GL;  // LM head, streamed in chunks of MAXSEG per wave
   static_assert(D % HD == 0 && D <= 1600, "model width");
+  static_assert(GQ::RPW <= 64 && GP::RPW <= 64 && GF::RPW <= 64 && GM::RPW <= 64, "one bias per leader lane");
   static_assert(GQ::SEGS <= PART_MAX && GF::SEGS <= PART_MAX && GM::SEGS <= PART_MAX && GL::SEGS <= PART_MAX,
                 "segment partials exceed LDS");
   static_assert(H <= MAX_ITEMS, "heads");
@@ -176,6 +193,22 @@ __device__ __forceinline__ float wsum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// Wave-wide sum through DPP (no LDS round trips): butterfly within each
+// 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_ror:4, row_ror:8), then the
+// four row sums are read out with v_readlane. Returns a wave-uniform value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wsum_dpp(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  const int b = __float_as_int(v);
+  return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+         (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
 __device__ __forceinline__ float wmax(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -222,8 +255,8 @@ struct V16<W_BF16> {
 // ---------------------------------------------------------------------------
 
 template <int WT, int MAXSEG, class GEO>
-__device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], const void* W, int wg, int cw, int lane,
-                                          int seg_base) {
+__device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], const void* W, const void* dummy, int wg,
+                                          int cw, int lane, int seg_base) {
   typedef typename V16<WT>::T Vec;
   const int row0 = wg * GEO::RPW;
   const int rows_here = min(GEO::RPW, GEO::N - row0);
@@ -232,12 +265,15 @@ __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], co
   const int nseg = min(GEO::SPW, segs_here - s0);
   int lr = s0 / GEO::SPR, j = s0 - lr * GEO::SPR;
   const Vec* base = reinterpret_cast<const Vec*>(W) + (long)row0 * GEO::VR;
+  // Branch-free: the compiler's wait-count analysis then sees a fixed load
+  // order and waits only for the buffer being consumed. Segments this wave
+  // does not own read a small zero page instead (L2-resident).
 #pragma unroll
   for (int i = 0; i < MAXSEG; ++i) {
-    if (i < GEO::SPW && i < nseg) {
-      const Vec* rowp = base + (long)lr * GEO::VR + j * 64;
-      if (GEO::VR % 64 == 0 || j * 64 + 64 <= GEO::VR) buf[i] = PK_G(Vec, rowp)[lane];
-      else buf[i] = PK_G(Vec, rowp)[min(lane, GEO::VR - j * 64 - 1)];
+    if (i < GEO::SPW) {
+      const Vec* rowp = i < nseg ? base + (long)lr * GEO::VR + j * 64 : reinterpret_cast<const Vec*>(dummy);
+      const int li = (GEO::VR % 64 == 0) ? lane : min(lane, max(0, min(GEO::VR - j * 64, 64) - 1));
+      buf[i] = PK_G(Vec, rowp)[li];
     }
     if (++j == GEO::SPR) {
       j = 0;
@@ -258,11 +294,11 @@ __device__ __forceinline__ void seg_compute(const typename V16<WT>::T (&buf)[MAX
   int j = s0 % GEO::SPR;
 #pragma unroll
   for (int i = 0; i < MAXSEG; ++i) {
-    if (i < GEO::SPW && i < nseg) {
+    if (i < GEO::SPW) {
       const int v = j * 64 + lane;
       const float d = V16<WT>::dot(buf[i], x + min(v, GEO::VR - 1) * E);
-      const float acc = wsum(v < GEO::VR ? d : 0.f);
-      if (lane == 0) part[s0 + i] = acc;
+      const float acc = wsum_dpp(v < GEO::VR ? d : 0.f);
+      if (lane == 0 && i < nseg) part[s0 + i] = acc;
     }
     if (++j == GEO::SPR) j = 0;
   }
@@ -280,37 +316,43 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
   const int wg = blockIdx.x;
   Vec A[MS], B[MS];
   unsigned seq = 0;
-  const LayerPtrs* LP = p.layers;
-  seg_issue<WT, MS, GQ>(A, LP[0].wqkv, wg, cw, lane, 0);
-  seg_issue<WT, MS, GP>(B, LP[0].waproj, wg, cw, lane, 0);
-  for (int l = 0; l < p.L; ++l) {
-    const bool last = l + 1 == p.L;
-    // QKV from A; refill A with this layer's FC weights
+  const void* dz = p.dummy;
+  // Layer pointers come through scalar loads (constant address space): a
+  // vector load would need a vmcnt wait that also drains the prefetch.
+  const __attribute__((address_space(4))) LayerPtrs* LP = PK_C(LayerPtrs, p.layers);
+  // The code below issues every buffer refill unconditionally (the last
+  // layer is peeled) so each consume waits only for its own buffer.
+  auto compute_and_signal = [&](auto& buf, const float* x, auto geo_tag) {
+    typedef decltype(geo_tag) GEO;
     lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
-    seg_compute<WT, MS, GQ>(A, sm.in_vec[1], sm.part, wg, cw, lane, 0);
+    if (cw == 0) PK_TRACE(p, 1024 + 2 * (int)seq, lane);
+    seg_compute<WT, MS, GEO>(buf, x, sm.part, wg, cw, lane, 0);
+    if (cw == 0) PK_TRACE(p, 1025 + 2 * (int)seq, lane);
     lds_release();
     if (lane == 0) lds_add(&sm.gemv_done, 1);
-    seg_issue<WT, MS, GF>(A, LP[l].wfc, wg, cw, lane, 0);
-    // attention projection from B; refill B with the MLP projection
-    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
-    seg_compute<WT, MS, GP>(B, sm.in_vec[0], sm.part, wg, cw, lane, 0);
-    lds_release();
-    if (lane == 0) lds_add(&sm.gemv_done, 1);
-    seg_issue<WT, MS, GM>(B, LP[l].wmproj, wg, cw, lane, 0);
-    // FC from A; refill A with the next layer's QKV (or the LM head's chunk 0)
-    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
-    seg_compute<WT, MS, GF>(A, sm.in_vec[1], sm.part, wg, cw, lane, 0);
-    lds_release();
-    if (lane == 0) lds_add(&sm.gemv_done, 1);
-    if (!last) seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, wg, cw, lane, 0);
-    else seg_issue<WT, MS, GL>(A, p.wte, wg, cw, lane, 0);
-    // MLP projection from B; refill B with the next layer's attention projection (or LM chunk 1)
-    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
-    seg_compute<WT, MS, GM>(B, sm.in_vec[0], sm.part, wg, cw, lane, 0);
-    lds_release();
-    if (lane == 0) lds_add(&sm.gemv_done, 1);
-    if (!last) seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, wg, cw, lane, 0);
-    else seg_issue<WT, MS, GL>(B, p.wte, wg, cw, lane, NC * GL::SPW);
+  };
+  seg_issue<WT, MS, GQ>(A, LP[0].wqkv, dz, wg, cw, lane, 0);
+  seg_issue<WT, MS, GP>(B, LP[0].waproj, dz, wg, cw, lane, 0);
+  for (int l = 0; l + 1 < p.L; ++l) {
+    compute_and_signal(A, sm.in_vec[1], GQ());   // QKV; refill A with FC
+    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0);
+    compute_and_signal(B, sm.in_vec[0], GP());   // attention projection; refill B with MLP projection
+    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0);
+    compute_and_signal(A, sm.in_vec[1], GF());   // FC; refill A with next QKV
+    seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0);
+    compute_and_signal(B, sm.in_vec[0], GM());   // MLP projection; refill B with next attention projection
+    seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0);
+  }
+  {  // last layer: the refills after FC / MLP projection are the LM head's chunks 0 and 1
+    const int l = p.L - 1;
+    compute_and_signal(A, sm.in_vec[1], GQ());
+    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0);
+    compute_and_signal(B, sm.in_vec[0], GP());
+    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0);
+    compute_and_signal(A, sm.in_vec[1], GF());
+    seg_issue<WT, MS, GL>(A, p.wte, dz, wg, cw, lane, 0);
+    compute_and_signal(B, sm.in_vec[0], GM());
+    seg_issue<WT, MS, GL>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW);
   }
   // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
   // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
@@ -320,11 +362,9 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
   const int segs_here = rows_here > 0 ? rows_here * GL::SPR : 0;
   for (int base = 0; base < segs_here; base += 2 * PER_CHUNK) {
     seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base);
-    if (base + 2 * PER_CHUNK < segs_here) seg_issue<WT, MS, GL>(A, p.wte, wg, cw, lane, base + 2 * PER_CHUNK);
-    if (base + PER_CHUNK < segs_here) {
-      seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK);
-      if (base + 3 * PER_CHUNK < segs_here) seg_issue<WT, MS, GL>(B, p.wte, wg, cw, lane, base + 3 * PER_CHUNK);
-    }
+    seg_issue<WT, MS, GL>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
+    seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK);
+    seg_issue<WT, MS, GL>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
   }
   lds_release();
   if (lane == 0) lds_add(&sm.gemv_done, 1);
@@ -342,17 +382,57 @@ __device__ __forceinline__ void glue_barrier(Smem<D>& sm, unsigned& gen, int lan
   lds_wait_ge(&sm.glue_cnt, gen * NGLUE, err);
 }
 
-// All glue lanes poll n tagged words into dst, MAXW words per lane per round
-// (all loads of a round in flight together).
-__device__ __forceinline__ void glue_poll(const u64* src, int n, unsigned tag, float* dst, int gl, unsigned* err) {
+__device__ __forceinline__ unsigned fload(const unsigned* p) {
+  return __hip_atomic_load(PK_GW(unsigned, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void fstore(unsigned* p, unsigned tag) {
+  __hip_atomic_store(PK_GW(unsigned, p), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Leader: raise this workgroup's flag once its data stores have completed
+// (s_waitcnt vmcnt(0) of the leader wave only; it holds no prefetch loads),
+// so readers that saw the flag find current tags on their first read.
+__device__ __forceinline__ void raise_flag(unsigned* f, unsigned tag, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if (lane == 0) fstore(f, tag);
+}
+
+// All glue lanes fetch n tagged words into dst. Exchange protocol:
+//  1. poll the producers' flag words (one 32-bit word per producer, coherent
+//     loads) until each carries `tag` - cheap to poll, unlike the data;
+//  2. read the data once with coherent loads;
+//  3. any word whose tag is still stale is re-read until it matches.
+// Correctness rests on the per-word tags alone; the flags only keep the
+// polling traffic to one 32-bit word per producer.
+__device__ __forceinline__ void glue_fetch(const unsigned* flags, int nprod, const u64* src, int n, unsigned tag,
+                                           float* dst, int gl, unsigned* err, const Params& p, int tidx) {
   constexpr int NG = NGLUE * 64;
-  const bool skip = err_set(err);
+  static_assert(NG * 2 >= G && NG * 2 >= MAX_ITEMS, "two flags per glue lane");
+  bool skip = false;
+  {
+    // both of this lane's flags in flight together; re-poll until current
+    const int i0 = gl, i1 = gl + NG;
+    unsigned f0 = i0 < nprod ? fload(flags + i0) : tag;
+    unsigned f1 = i1 < nprod ? fload(flags + i1) : tag;
+    unsigned spins = 0;
+    while (f0 != tag || f1 != tag) {
+      if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(err))) {
+        raise_err(err, 1u);
+        skip = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      if (f0 != tag) f0 = fload(flags + i0);
+      if (f1 != tag) f1 = fload(flags + i1);
+    }
+  }
+  if (gl < 64) PK_TRACE(p, tidx, gl);
   for (int base = 0; base < n; base += MAXW * NG) {
     u64 w[MAXW];
 #pragma unroll
     for (int k = 0; k < MAXW; ++k) {
       const int i = base + gl + k * NG;
-      w[k] = (i < n && !skip) ? tload(src + i) : ((u64)tag << 32);
+      w[k] = (i < n && !skip) ? PK_G(u64, src)[i] : ((u64)tag << 32);
     }
     unsigned spins = 0;
     for (;;) {
@@ -380,21 +460,44 @@ __device__ __forceinline__ void glue_poll(const u64* src, int n, unsigned tag, f
   }
 }
 
+// LayerNorm gain/bias of this lane's columns, loaded ahead of the input poll.
+template <int D>
+struct LnParams {
+  static constexpr int NK = D / 64;
+  float w[NK], b[NK];
+};
+template <int D>
+__device__ __forceinline__ void ln_prefetch(LnParams<D>& q, const float* w, const float* b, int lane) {
+#pragma unroll
+  for (int k = 0; k < LnParams<D>::NK; ++k) {
+    q.w[k] = PK_G(float, w)[lane + 64 * k];
+    q.b[k] = PK_G(float, b)[lane + 64 * k];
+  }
+}
+
 // Leader only: LayerNorm of src[D] into dst (gpt2.rs:636-666, two-pass).
 template <int D>
-__device__ __forceinline__ void leader_layernorm(const float* src, const float* w, const float* b, float eps,
-                                                 float* dst, int lane) {
+__device__ __forceinline__ void leader_layernorm(const float* src, const LnParams<D>& q, float eps, float* dst,
+                                                 int lane) {
+  constexpr int NK = LnParams<D>::NK;
+  float x[NK];
   float s = 0.f;
-  for (int i = lane; i < D; i += 64) s += src[i];
-  const float mean = wsum(s) / (float)D;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    x[k] = src[lane + 64 * k];
+    s += x[k];
+  }
+  const float mean = wsum_dpp(s) / (float)D;
   float v = 0.f;
-  for (int i = lane; i < D; i += 64) {
-    const float t = src[i] - mean;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const float t = x[k] - mean;
     v += t * t;
   }
-  const float var = wsum(v) / (float)D;
+  const float var = wsum_dpp(v) / (float)D;
   const float inv_std = 1.0f / sqrtf(var + eps);
-  for (int i = lane; i < D; i += 64) dst[i] = (src[i] - mean) * inv_std * PK_G(float, w)[i] + PK_G(float, b)[i];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) dst[lane + 64 * k] = (x[k] - mean) * inv_std * q.w[k] + q.b[k];
 }
 
 // Leader only: publish in_vec to the GEMV waves and wait for their partials.
@@ -431,6 +534,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   const int pos = len - 1;
   // embedding (gpt2.rs:377-384): every workgroup computes x0 itself
   if (leader) {
+    PK_TRACE(p, 0, lane);
     const uint32_t tok = *PK_G(uint32_t, p.token);
     for (int i = lane; i < D; i += 64) {
       float w;
@@ -444,22 +548,35 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   const int CL = (len + NCH - 1) / NCH;
   const int j0 = ic * CL, j1 = min(len, j0 + CL);
   for (int l = 0; l < p.L; ++l) {
-    const LayerPtrs& LP = p.layers[l];
+    const __attribute__((address_space(4))) LayerPtrs& LP = PK_C(LayerPtrs, p.layers)[l];
     u64* T = p.tag + (long)l * p.lw;
+    unsigned* FL = p.flags + (long)l * p.fl;
     // ---- QKV: LN1(x) @ c_attn + bias; k/v of the new token into the cache ----
+    const int tb = 1 + 16 * l;  // trace index base of this layer
+    // parameters of this phase, loaded before waiting for its input
+    LnParams<D> lnq;
+    float bias = 0.f;
+    if (leader) {
+      ln_prefetch<D>(lnq, LP.ln1w, LP.ln1b, lane);
+      const int row0 = wg * GQ::RPW, rows_here = min(GQ::RPW, GQ::N - row0);
+      if (lane < rows_here) bias = PK_G(float, LP.bqkv)[row0 + lane];
+    }
     if (l > 0) {
-      glue_poll(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
+      glue_fetch(p.flags + (long)(l - 1) * p.fl + F_X3, G, p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw,
+                 gl, p.err, p, -1);
       glue_barrier(sm, gen, lane, p.err);
     }
     if (leader) {
-      leader_layernorm<D>(sm.xraw, LP.ln1w, LP.ln1b, p.eps, sm.in_vec[1], lane);
+      PK_TRACE(p, tb + 0, lane);
+      leader_layernorm<D>(sm.xraw, lnq, p.eps, sm.in_vec[1], lane);
       leader_run_gemv(sm, seq, lane, p.err);
+      PK_TRACE(p, tb + 1, lane);
       const int row0 = wg * GQ::RPW, rows_here = min(GQ::RPW, GQ::N - row0);
       float* kl = p.kc + (long)l * p.kv_layer;
       float* vl = p.vc + (long)l * p.kv_layer;
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
-        const float v = row_acc<GQ>(sm, lr) + PK_G(float, LP.bqkv)[n];
+        const float v = row_acc<GQ>(sm, lr) + bias;
         tstore(T + p.o_qkv + n, v, tag);
         if (n >= D) {
           const int c = n < 2 * D ? n - D : n - 2 * D;
@@ -468,26 +585,30 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
           PK_GW(float, base)[((long)h * p.P + pos) * HD + dd] = v;
         }
       }
+      PK_TRACE(p, tb + 2, lane);
     }
     // ---- attention (multi_head_attention_cached, gpt2.rs:772-834): one item
     //      per workgroup = head ih, positions [j0, j1) ----
     if (item >= 0) {
       if (leader) {
-        float* dsts[3] = {sm.att_q, sm.att_k, sm.att_v};
-        for (int part = 0; part < 3; ++part) {
-          const u64* src = T + p.o_qkv + part * D + ih * HD;
-          u64 w = tload(src + lane);
-          unsigned spins = 0;
-          while ((unsigned)(w >> 32) != tag) {
-            if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(p.err))) {
-              raise_err(p.err, 1u);
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-            w = tload(src + lane);
+        // q, k_new, v_new of head ih: all three loads in flight, then re-poll
+        const u64* src = T + p.o_qkv + ih * HD + lane;
+        u64 wq = tload(src), wk = tload(src + D), wv = tload(src + 2 * D);
+        unsigned spins = 0;
+        while ((unsigned)(wq >> 32) != tag || (unsigned)(wk >> 32) != tag || (unsigned)(wv >> 32) != tag) {
+          if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(p.err))) {
+            raise_err(p.err, 1u);
+            break;
           }
-          dsts[part][lane] = __uint_as_float((unsigned)w);
+          __builtin_amdgcn_s_sleep(1);
+          if ((unsigned)(wq >> 32) != tag) wq = tload(src);
+          if ((unsigned)(wk >> 32) != tag) wk = tload(src + D);
+          if ((unsigned)(wv >> 32) != tag) wv = tload(src + 2 * D);
         }
+        sm.att_q[lane] = __uint_as_float((unsigned)wq);
+        sm.att_k[lane] = __uint_as_float((unsigned)wk);
+        sm.att_v[lane] = __uint_as_float((unsigned)wv);
+        PK_TRACE(p, tb + 3, lane);
       }
       glue_barrier(sm, gen, lane, p.err);
       if (!leader) {
@@ -496,43 +617,53 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         const int a0 = j0 + hw * per, a1 = min(j1, a0 + per);
         const float* Kh = p.kc + (long)l * p.kv_layer + (long)ih * p.P * HD;
         const float* Vh = p.vc + (long)l * p.kv_layer + (long)ih * p.P * HD;
+        // 16 lanes per position (4 dims each), 4 positions per row of the
+        // wave, AT positions-groups per block: all K and V rows of a block
+        // are loaded together, then an online-softmax update per block.
+        constexpr int AT = 8;
         const int grp = lane >> 4, dq = (lane & 15) * 4;
         const float scale = 0.125f;  // 1 / sqrt(64)
         const float4 q4 = *reinterpret_cast<const float4*>(sm.att_q + dq);
-        float mloc = -INFINITY;
-        for (int jb = a0; jb < a1; jb += 4) {  // 4 positions per iteration, 16 lanes each
-          const int j = jb + grp;
-          float dot = 0.f;
-          if (j < a1) {
-            const float4 k4 = j == pos ? *reinterpret_cast<const float4*>(sm.att_k + dq)
-                                       : ld4g(Kh + (long)j * HD + dq);
-            dot = q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
-          }
-#pragma unroll
-          for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
-          float s = -INFINITY;
-          if (j < a1) {
-            s = dot * scale;
-            if ((lane & 15) == 0) sm.att_s[hw][j - a0] = s;
-          }
-          mloc = fmaxf(mloc, s);
-        }
-        const float m = wmax(mloc);
-        lds_release();
-        lds_acquire();
-        float lsum = 0.f;
+        float m = -INFINITY, lsum = 0.f;
         float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int jb = a0; jb < a1; jb += 4) {
-          const int j = jb + grp;
-          if (j >= a1) continue;
-          const float pj = expf(sm.att_s[hw][j - a0] - m);
-          const float4 v4 = j == pos ? *reinterpret_cast<const float4*>(sm.att_v + dq)
-                                     : ld4g(Vh + (long)j * HD + dq);
-          if ((lane & 15) == 0) lsum += pj;
-          o4.x += pj * v4.x;
-          o4.y += pj * v4.y;
-          o4.z += pj * v4.z;
-          o4.w += pj * v4.w;
+        for (int jb = a0; jb < a1; jb += 4 * AT) {
+          float4 k4[AT], v4[AT];
+#pragma unroll
+          for (int t = 0; t < AT; ++t) {
+            const int j = min(jb + 4 * t + grp, a1 - 1);
+            k4[t] = j == pos ? *reinterpret_cast<const float4*>(sm.att_k + dq) : ld4g(Kh + (long)j * HD + dq);
+            v4[t] = j == pos ? *reinterpret_cast<const float4*>(sm.att_v + dq) : ld4g(Vh + (long)j * HD + dq);
+          }
+          float s[AT];
+          float mb = -INFINITY;
+#pragma unroll
+          for (int t = 0; t < AT; ++t) {
+            float dot = q4.x * k4[t].x + q4.y * k4[t].y + q4.z * k4[t].z + q4.w * k4[t].w;
+            dot += dpp_mov<0xB1>(dot);  // sum over the 16 lanes of this position (one DPP row)
+            dot += dpp_mov<0x4E>(dot);
+            dot += dpp_mov<0x124>(dot);
+            dot += dpp_mov<0x128>(dot);
+            s[t] = (jb + 4 * t + grp < a1) ? dot * scale : -INFINITY;
+            mb = fmaxf(mb, s[t]);
+          }
+          mb = wmax(mb);
+          const float mn = fmaxf(m, mb);
+          const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+          lsum *= corr;
+          o4.x *= corr;
+          o4.y *= corr;
+          o4.z *= corr;
+          o4.w *= corr;
+#pragma unroll
+          for (int t = 0; t < AT; ++t) {
+            const float pj = s[t] == -INFINITY ? 0.f : expf(s[t] - mn);
+            if ((lane & 15) == 0) lsum += pj;
+            o4.x += pj * v4[t].x;
+            o4.y += pj * v4[t].y;
+            o4.z += pj * v4[t].z;
+            o4.w += pj * v4[t].w;
+          }
+          m = mn;
         }
         lsum = wsum(lsum);
 #pragma unroll
@@ -555,6 +686,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       }
       glue_barrier(sm, gen, lane, p.err);
       if (leader) {  // merge the helpers' (m, l, o) into the item's partial softmax
+        PK_TRACE(p, tb + 4, lane);
         float M = -INFINITY;
         for (int w = 0; w < NA; ++w) M = fmaxf(M, sm.att_part[w][0]);
         float Ls = 0.f, o = 0.f;
@@ -571,62 +703,95 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
           tstore(dst, M, tag);
           tstore(dst + 1, Ls, tag);
         }
+        raise_flag(FL + F_ATT + item, tag, lane);
       }
     }
     // ---- attention projection + residual (gpt2.rs:523-526) ----
-    glue_poll(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
+    if (leader) {
+      const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
+      bias = lane < rows_here ? PK_G(float, LP.baproj)[row0 + lane] : 0.f;
+    }
+    glue_fetch(FL + F_ATT, items, T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err, p, tb + 14);
+    glue_barrier(sm, gen, lane, p.err);
+    // merge the chunks of each head; heads are spread over the glue waves
+    for (int h = gw; h < H; h += NGLUE) {
+      float M = -INFINITY;
+      for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS]);
+      float Ls = 0.f, o = 0.f;
+      for (int c = 0; c < NCH; ++c) {
+        const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
+        if (it[0] == -INFINITY) continue;
+        const float f = expf(it[0] - M);
+        Ls += it[1] * f;
+        o += it[2 + lane] * f;
+      }
+      sm.in_vec[0][h * HD + lane] = o / Ls;
+    }
     glue_barrier(sm, gen, lane, p.err);
     if (leader) {
-      for (int h = 0; h < H; ++h) {  // merge the chunks of each head
-        float M = -INFINITY;
-        for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS]);
-        float Ls = 0.f, o = 0.f;
-        for (int c = 0; c < NCH; ++c) {
-          const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
-          if (it[0] == -INFINITY) continue;
-          const float f = expf(it[0] - M);
-          Ls += it[1] * f;
-          o += it[2 + lane] * f;
-        }
-        sm.in_vec[0][h * HD + lane] = o / Ls;
-      }
+      PK_TRACE(p, tb + 5, lane);
       leader_run_gemv(sm, seq, lane, p.err);
+      PK_TRACE(p, tb + 6, lane);
       const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
-        tstore(T + p.o_x2 + n, sm.xraw[n] + (row_acc<GP>(sm, lr) + PK_G(float, LP.baproj)[n]), tag);
+        tstore(T + p.o_x2 + n, sm.xraw[n] + (row_acc<GP>(sm, lr) + bias), tag);
       }
+      raise_flag(FL + F_X2 + wg, tag, lane);
+      PK_TRACE(p, tb + 7, lane);
     }
     // ---- FC + gelu_new (gpt2.rs:529-533) ----
-    glue_poll(T + p.o_x2, D, tag, sm.x2raw, gl, p.err);
+    if (leader) {
+      ln_prefetch<D>(lnq, LP.ln2w, LP.ln2b, lane);
+      const int row0 = wg * GF::RPW, rows_here = min(GF::RPW, GF::N - row0);
+      bias = lane < rows_here ? PK_G(float, LP.bfc)[row0 + lane] : 0.f;
+    }
+    glue_fetch(FL + F_X2, G, T + p.o_x2, D, tag, sm.x2raw, gl, p.err, p, -1);
     glue_barrier(sm, gen, lane, p.err);
     if (leader) {
-      leader_layernorm<D>(sm.x2raw, LP.ln2w, LP.ln2b, p.eps, sm.in_vec[1], lane);
+      PK_TRACE(p, tb + 8, lane);
+      leader_layernorm<D>(sm.x2raw, lnq, p.eps, sm.in_vec[1], lane);
       leader_run_gemv(sm, seq, lane, p.err);
+      PK_TRACE(p, tb + 9, lane);
       const int row0 = wg * GF::RPW, rows_here = min(GF::RPW, GF::N - row0);
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
-        tstore(T + p.o_h + n, gelu_new(row_acc<GF>(sm, lr) + PK_G(float, LP.bfc)[n]), tag);
+        tstore(T + p.o_h + n, gelu_new(row_acc<GF>(sm, lr) + bias), tag);
       }
+      raise_flag(FL + F_H + wg, tag, lane);
+      PK_TRACE(p, tb + 10, lane);
     }
     // ---- MLP projection + residual (gpt2.rs:534-537) ----
-    glue_poll(T + p.o_h, 4 * D, tag, sm.in_vec[0], gl, p.err);
+    if (leader) {
+      const int row0 = wg * GM::RPW, rows_here = min(GM::RPW, GM::N - row0);
+      bias = lane < rows_here ? PK_G(float, LP.bmproj)[row0 + lane] : 0.f;
+    }
+    glue_fetch(FL + F_H, G, T + p.o_h, 4 * D, tag, sm.in_vec[0], gl, p.err, p, tb + 15);
     glue_barrier(sm, gen, lane, p.err);
     if (leader) {
+      PK_TRACE(p, tb + 11, lane);
       leader_run_gemv(sm, seq, lane, p.err);
+      PK_TRACE(p, tb + 12, lane);
       const int row0 = wg * GM::RPW, rows_here = min(GM::RPW, GM::N - row0);
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
-        tstore(T + p.o_x3 + n, sm.x2raw[n] + (row_acc<GM>(sm, lr) + PK_G(float, LP.bmproj)[n]), tag);
+        tstore(T + p.o_x3 + n, sm.x2raw[n] + (row_acc<GM>(sm, lr) + bias), tag);
       }
+      raise_flag(FL + F_X3 + wg, tag, lane);
+      PK_TRACE(p, tb + 13, lane);
     }
   }
   // ---- ln_f + tied LM head + argmax (gpt2.rs:392-396, 858-868) ----
-  glue_poll(p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
+  LnParams<D> lnf;
+  if (leader) ln_prefetch<D>(lnf, p.lnfw, p.lnfb, lane);
+  glue_fetch(p.flags + (long)(p.L - 1) * p.fl + F_X3, G, p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw,
+             gl, p.err, p, 4 + 16 * p.L);
   glue_barrier(sm, gen, lane, p.err);
   if (leader) {
-    leader_layernorm<D>(sm.xraw, p.lnfw, p.lnfb, p.eps, sm.in_vec[1], lane);
+    PK_TRACE(p, 1 + 16 * p.L, lane);
+    leader_layernorm<D>(sm.xraw, lnf, p.eps, sm.in_vec[1], lane);
     leader_run_gemv(sm, seq, lane, p.err);
+    PK_TRACE(p, 2 + 16 * p.L, lane);
     const int row0 = wg * GL::RPW, rows_here = min(GL::RPW, GL::N - row0);
     u64 best = 0ull;
     for (int lr = lane; lr < rows_here; lr += 64) {
@@ -648,6 +813,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
     }
     if (lane == 0 && best != 0ull)
       __hip_atomic_fetch_max(PK_GW(u64, p.keys), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    PK_TRACE(p, 3 + 16 * p.L, lane);
   }
 }
 

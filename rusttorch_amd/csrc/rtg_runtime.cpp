@@ -419,6 +419,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   HIPX(hipMemcpyAsync(gen.data(), c->ids_dev, B * P * 4, hipMemcpyDeviceToHost, s));
   HIPX(hipStreamSynchronize(s));
   if (c->pstate) {
+    persistent_dump_trace(c->pstate);
     unsigned e = 0;
     HIPX(hipMemcpy(&e, persistent_err(c->pstate), 4, hipMemcpyDeviceToHost));
     if (e) {
