@@ -53,7 +53,6 @@ struct PersistentState {
   unsigned* epoch = nullptr;
   unsigned* err = nullptr;
   pk::u64* trace = nullptr;
-  unsigned* flags = nullptr;
 };
 
 PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
@@ -70,14 +69,6 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   for (const Inst& in : kInstances)
     if (in.d == d && in.v == V && in.wtype == w.wtype) fn = in.fn();
   if (!fn) return pl;
-  {
-    // positions per helper wave at the smallest chunk count must fit in LDS
-    const int cap0 = pk::CMAX < pk::MAX_ITEMS / H ? pk::CMAX : pk::MAX_ITEMS / H;
-    const int cap = cap0 < pk::G / H ? cap0 : pk::G / H;
-    const int capc = cap < 1 ? 1 : cap;
-    const int per = ((P + capc - 1) / capc + pk::NA - 1) / pk::NA;
-    if (per > pk::ATT_POS_MAX) return pl;
-  }
   std::vector<pk::LayerPtrs> lp(L);
   for (int i = 0; i < L; ++i) {
     const PersistentLayer& s = w.layers[i];
@@ -98,13 +89,15 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   p.P = P;
   p.eps = w.cfg.layer_norm_epsilon;
   p.kv_layer = (long)H * P * pk::HD;
-  // tagged exchange buffers of one layer
+  // Tagged exchange regions of one layer: one slot of whole 128-byte lines per
+  // producer (workgroup rows of a GEMV phase, or one attention item).
+  auto region = [](int n) { return pk::G * pk::slot_words((n + pk::G - 1) / pk::G); };
   p.o_qkv = 0;
-  p.o_att = 3 * d;
-  p.o_x2 = p.o_att + pk::MAX_ITEMS * pk::ITEM_WORDS;
-  p.o_h = p.o_x2 + d;
-  p.o_x3 = p.o_h + 4 * d;
-  p.lw = (p.o_x3 + d + 63) / 64 * 64;
+  p.o_att = region(3 * d);
+  p.o_x2 = p.o_att + pk::MAX_ITEMS * pk::ITEM_SLOT;
+  p.o_h = p.o_x2 + region(d);
+  p.o_x3 = p.o_h + region(4 * d);
+  p.lw = p.o_x3 + region(d);
   pl->kernel = fn;
   return pl;
 }
@@ -131,15 +124,13 @@ PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, floa
   s->p = pl->base;
   pk::Params& p = s->p;
   const size_t words = (size_t)p.lw * p.L;
-  const size_t nflags = (size_t)pk::F_LAYER * p.L;
   if (hipMalloc(&s->tags, words * 8) != hipSuccess || hipMalloc(&s->epoch, 256) != hipSuccess ||
-      hipMalloc(&s->err, 256) != hipSuccess || hipMalloc(&s->flags, nflags * 4) != hipSuccess) {
+      hipMalloc(&s->err, 256) != hipSuccess) {
     persistent_state_destroy(s);
     return nullptr;
   }
   // tag 0 never matches: the epoch starts at 1 and only grows
-  if (hipMemset(s->tags, 0, words * 8) != hipSuccess || hipMemset(s->err, 0, 256) != hipSuccess ||
-      hipMemset(s->flags, 0, nflags * 4) != hipSuccess) {
+  if (hipMemset(s->tags, 0, words * 8) != hipSuccess || hipMemset(s->err, 0, 256) != hipSuccess) {
     persistent_state_destroy(s);
     return nullptr;
   }
@@ -149,8 +140,6 @@ PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, floa
     return nullptr;
   }
   p.tag = s->tags;
-  p.flags = s->flags;
-  p.fl = pk::F_LAYER;
   p.epoch = s->epoch;
   p.err = s->err;
   p.trace = nullptr;
@@ -175,7 +164,6 @@ void persistent_state_destroy(PersistentState* s) {
   if (s->epoch) hipFree(s->epoch);
   if (s->err) hipFree(s->err);
   if (s->trace) hipFree(s->trace);
-  if (s->flags) hipFree(s->flags);
   delete s;
 }
 

@@ -46,9 +46,16 @@ constexpr int HD = 64;              // head_dim of every GPT-2 size
 constexpr int CMAX = 16;            // attention chunks per head
 constexpr int ITEM_WORDS = 2 + HD;  // m, l, o[64]
 constexpr int MAX_ITEMS = 64;       // heads * chunks merged by the consumers
-constexpr int MAXW = 12;            // polled words per glue lane per round
+constexpr int MAXW = 16;            // polled words per glue lane per round
 constexpr int PART_MAX = 1536;      // segment partials per workgroup
-constexpr int ATT_POS_MAX = 256;    // positions per helper wave per item
+constexpr int KVS = 128;            // cached positions of one item staged in LDS
+// Exchange layout: each producer owns a slot of whole 128-byte lines, so no
+// two producers ever write the same line and readers of one producer's words
+// touch only that producer's lines (lines written by many producers and read
+// by all 256 workgroups were measured to double the exchange latency).
+constexpr int LINE_WORDS = 16;  // u64 words per 128-byte line
+__host__ __device__ constexpr int slot_words(int rows) { return (rows + LINE_WORDS - 1) / LINE_WORDS * LINE_WORDS; }
+constexpr int ITEM_SLOT = slot_words(ITEM_WORDS);  // words of one attention item's slot
 constexpr unsigned SPIN_CAP = 1u << 21;
 
 typedef unsigned long long u64;
@@ -76,9 +83,7 @@ struct Params {
   const unsigned* epoch;
   u64* tag;  // tagged words, lw per layer
   long lw;
-  int o_qkv, o_att, o_x2, o_h, o_x3;
-  unsigned* flags;  // producer flags, fl per layer: x2[G], h[G], x3[G], att[MAX_ITEMS]
-  long fl;
+  int o_qkv, o_att, o_x2, o_h, o_x3;  // exchange regions of a layer (words)
   float* logits;
   u64* keys;
   unsigned* err;
@@ -86,15 +91,18 @@ struct Params {
   const void* dummy;  // >= 1 KiB of zeros: target of the loads of segments a wave does not own
 };
 
+// Optional phase trace (p.trace != null): timestamps of the 100 MHz constant
+// clock relative to the workgroup's start, kept in LDS so that tracing adds
+// no global stores (and no memory-counter waits) to the traced paths, and
+// written to p.trace[wg * TRACE_STRIDE + idx] (absolute, u64) at the end.
+// Index spaces: [0, 16L+4) layer/LM-head points of the leader, 800 + 4l + k
+// helper/LayerNorm points, 1024 + 2*seq (+1) GEMV start/end of phase seq.
 constexpr int TRACE_STRIDE = 2048;
-// flag array offsets within a layer's flags
-constexpr int F_X2 = 0, F_H = G, F_X3 = 2 * G, F_ATT = 3 * G, F_LAYER = 3 * G + MAX_ITEMS;
-
-// Timestamp (100 MHz constant clock) of a trace point, written by lane 0.
-#define PK_TRACE(p, idx, lane)                                                                 \
-  do {                                                                                         \
-    if ((p).trace && (lane) == 0 && (idx) >= 0 && (idx) < TRACE_STRIDE)                                      \
-      PK_GW(u64, (p).trace)[(long)blockIdx.x * TRACE_STRIDE + (idx)] = wall_clock64();         \
+constexpr int TRACE_N = 1536;
+#define PK_TRACE(p, idx, lane)                                               \
+  do {                                                                       \
+    if ((p).trace && (lane) == 0 && (idx) >= 0 && (idx) < TRACE_N)           \
+      sm.trace_rel[(idx)] = (unsigned)(wall_clock64() - sm.trace_t0) | 1u;   \
   } while (0)
 
 // Row split of one GEMV phase: N outputs, each a dot product over K inputs
@@ -103,8 +111,15 @@ template <int N_, int K_, int E_, int SPW_ = 0>
 struct Geom {
   static constexpr int N = N_, K = K_, VR = K_ / E_, SPR = (VR + 63) / 64;
   static constexpr int RPW = (N_ + G - 1) / G;
+  static constexpr int SW = slot_words(RPW);  // exchange slot of one workgroup's rows
   static constexpr int SEGS = RPW * SPR;
-  static constexpr int SPW = SPW_ ? SPW_ : (SEGS + NC - 1) / NC;
+  // Segments per GEMV wave: an even split, rounded up to whole rows unless
+  // that would exceed max(12, even split) registers-worth of segments, so
+  // that each wave reduces whole rows with a compile-time structure.
+  static constexpr int SPW0 = (SEGS + NC - 1) / NC;
+  static constexpr int SPW_ROWS = (SPW0 + SPR - 1) / SPR * SPR;
+  static constexpr int SPW = SPW_ ? SPW_ : SPW_ROWS <= (SPW0 > 12 ? SPW0 : 12) ? SPW_ROWS : SPW0;
+  static constexpr bool ALIGNED = SPW % SPR == 0;  // every wave starts on a row
 };
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
@@ -133,9 +148,11 @@ struct Smem {
   float part[PART_MAX];
   float stage[MAX_ITEMS * ITEM_WORDS];
   float att_q[HD], att_k[HD], att_v[HD];
-  float att_s[NA][ATT_POS_MAX];
+  float kv_k[KVS * HD], kv_v[KVS * HD];  // K/V rows [j0, j0 + KVS) of this workgroup's item
   float att_part[NA][ITEM_WORDS];
   unsigned gemv_ready, gemv_done, glue_cnt;
+  u64 trace_t0;
+  unsigned trace_rel[TRACE_N];
 };
 
 // ---------------------------------------------------------------------------
@@ -254,9 +271,17 @@ struct V16<W_BF16> {
 // [seg_base + cw*SPW, seg_base + (cw+1)*SPW). All bookkeeping is scalar.
 // ---------------------------------------------------------------------------
 
-template <int WT, int MAXSEG, class GEO>
+#ifndef PK_PACE
+#define PK_PACE 12
+#endif
+// PACE > 0: sleep PACE*64 clocks between loads while the wave's next input
+// is not ready yet (*ready < next), so a refill does not flood this CU's
+// memory queue ahead of the exchanges; the sleep is the only conditional
+// part, the loads stay in fixed order.
+template <int WT, int MAXSEG, class GEO, int PACE = PK_PACE>
 __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], const void* W, const void* dummy, int wg,
-                                          int cw, int lane, int seg_base) {
+                                          int cw, int lane, int seg_base, unsigned* ready = nullptr,
+                                          unsigned next = 0) {
   typedef typename V16<WT>::T Vec;
   const int row0 = wg * GEO::RPW;
   const int rows_here = min(GEO::RPW, GEO::N - row0);
@@ -274,6 +299,7 @@ __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], co
       const Vec* rowp = i < nseg ? base + (long)lr * GEO::VR + j * 64 : reinterpret_cast<const Vec*>(dummy);
       const int li = (GEO::VR % 64 == 0) ? lane : min(lane, max(0, min(GEO::VR - j * 64, 64) - 1));
       buf[i] = PK_G(Vec, rowp)[li];
+      if (PACE > 0 && i + 1 < GEO::SPW && lds_load(ready) < next) __builtin_amdgcn_s_sleep(PACE);
     }
     if (++j == GEO::SPR) {
       j = 0;
@@ -291,16 +317,39 @@ __device__ __forceinline__ void seg_compute(const typename V16<WT>::T (&buf)[MAX
   const int segs_here = rows_here > 0 ? rows_here * GEO::SPR : 0;
   const int s0 = seg_base + cw * GEO::SPW;
   const int nseg = min(GEO::SPW, segs_here - s0);
-  int j = s0 % GEO::SPR;
+  if constexpr (GEO::ALIGNED) {
+    // The wave owns whole rows: each lane sums its products over a row's SPR
+    // segments and the wave reduces once per row. The row sum goes to the
+    // part slot of the row's last segment, zeros to the others. (Zero-page
+    // segments past nseg are whole rows too and are not stored.)
+    float run = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXSEG; ++i) {
-    if (i < GEO::SPW) {
+    for (int i = 0; i < GEO::SPW; ++i) {
+      const int j = i % GEO::SPR;
       const int v = j * 64 + lane;
       const float d = V16<WT>::dot(buf[i], x + min(v, GEO::VR - 1) * E);
-      const float acc = wsum_dpp(v < GEO::VR ? d : 0.f);
-      if (lane == 0 && i < nseg) part[s0 + i] = acc;
+      run += v < GEO::VR ? d : 0.f;
+      if (j == GEO::SPR - 1) {
+        const float acc = wsum_dpp(run);
+        run = 0.f;
+        if (lane == 0 && i < nseg) part[s0 + i] = acc;
+      } else if (lane == 0 && i < nseg) {
+        part[s0 + i] = 0.f;
+      }
     }
-    if (++j == GEO::SPR) j = 0;
+  } else {
+    // Rows span waves: one reduction per segment.
+    int j = s0 % GEO::SPR;
+#pragma unroll
+    for (int i = 0; i < MAXSEG; ++i) {
+      if (i < GEO::SPW) {
+        const int v = j * 64 + lane;
+        const float d = V16<WT>::dot(buf[i], x + min(v, GEO::VR - 1) * E);
+        const float acc = wsum_dpp(v < GEO::VR ? d : 0.f);
+        if (lane == 0 && i < nseg) part[s0 + i] = acc;
+      }
+      if (++j == GEO::SPR) j = 0;
+    }
   }
 }
 
@@ -331,28 +380,28 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     lds_release();
     if (lane == 0) lds_add(&sm.gemv_done, 1);
   };
-  seg_issue<WT, MS, GQ>(A, LP[0].wqkv, dz, wg, cw, lane, 0);
-  seg_issue<WT, MS, GP>(B, LP[0].waproj, dz, wg, cw, lane, 0);
+  seg_issue<WT, MS, GQ, 0>(A, LP[0].wqkv, dz, wg, cw, lane, 0);  // needed first: no pacing
+  seg_issue<WT, MS, GP>(B, LP[0].waproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
   for (int l = 0; l + 1 < p.L; ++l) {
     compute_and_signal(A, sm.in_vec[1], GQ());   // QKV; refill A with FC
-    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0);
+    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
     compute_and_signal(B, sm.in_vec[0], GP());   // attention projection; refill B with MLP projection
-    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0);
+    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
     compute_and_signal(A, sm.in_vec[1], GF());   // FC; refill A with next QKV
-    seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0);
+    seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
     compute_and_signal(B, sm.in_vec[0], GM());   // MLP projection; refill B with next attention projection
-    seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0);
+    seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
   }
   {  // last layer: the refills after FC / MLP projection are the LM head's chunks 0 and 1
     const int l = p.L - 1;
     compute_and_signal(A, sm.in_vec[1], GQ());
-    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0);
+    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
     compute_and_signal(B, sm.in_vec[0], GP());
-    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0);
+    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
     compute_and_signal(A, sm.in_vec[1], GF());
-    seg_issue<WT, MS, GL>(A, p.wte, dz, wg, cw, lane, 0);
+    seg_issue<WT, MS, GL>(A, p.wte, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
     compute_and_signal(B, sm.in_vec[0], GM());
-    seg_issue<WT, MS, GL>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW);
+    seg_issue<WT, MS, GL>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, &sm.gemv_ready, seq + 1);
   }
   // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
   // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
@@ -361,10 +410,11 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
   const int rows_here = min(GL::RPW, GL::N - wg * GL::RPW);
   const int segs_here = rows_here > 0 ? rows_here * GL::SPR : 0;
   for (int base = 0; base < segs_here; base += 2 * PER_CHUNK) {
+    // nothing else is in flight now: stream at full rate
     seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base);
-    seg_issue<WT, MS, GL>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
+    seg_issue<WT, MS, GL, 0>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
     seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK);
-    seg_issue<WT, MS, GL>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
+    seg_issue<WT, MS, GL, 0>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
   }
   lds_release();
   if (lane == 0) lds_add(&sm.gemv_done, 1);
@@ -382,57 +432,28 @@ __device__ __forceinline__ void glue_barrier(Smem<D>& sm, unsigned& gen, int lan
   lds_wait_ge(&sm.glue_cnt, gen * NGLUE, err);
 }
 
-__device__ __forceinline__ unsigned fload(const unsigned* p) {
-  return __hip_atomic_load(PK_GW(unsigned, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void fstore(unsigned* p, unsigned tag) {
-  __hip_atomic_store(PK_GW(unsigned, p), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Leader: raise this workgroup's flag once its data stores have completed
-// (s_waitcnt vmcnt(0) of the leader wave only; it holds no prefetch loads),
-// so readers that saw the flag find current tags on their first read.
-__device__ __forceinline__ void raise_flag(unsigned* f, unsigned tag, int lane) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  if (lane == 0) fstore(f, tag);
+// Address of word i of an exchange whose producers each publish RPW words
+// into slots of SW words.
+template <int RPW, int SW>
+__device__ __forceinline__ int slot_of(int i) {
+  return (i / RPW) * SW + i % RPW;
 }
 
-// All glue lanes fetch n tagged words into dst. Exchange protocol:
-//  1. poll the producers' flag words (one 32-bit word per producer, coherent
-//     loads) until each carries `tag` - cheap to poll, unlike the data;
-//  2. read the data once with coherent loads;
-//  3. any word whose tag is still stale is re-read until it matches.
-// Correctness rests on the per-word tags alone; the flags only keep the
-// polling traffic to one 32-bit word per producer.
-__device__ __forceinline__ void glue_fetch(const unsigned* flags, int nprod, const u64* src, int n, unsigned tag,
-                                           float* dst, int gl, unsigned* err, const Params& p, int tidx) {
+// All glue lanes fetch the n tagged words of an exchange into dst: every
+// word is read with a coherent load (never a stale line of this XCD's L2)
+// and stale words are re-read until their tags equal the step's epoch. The
+// data is polled directly: with one line per producer slot, a poll costs
+// the same line requests as polling a per-producer flag would, and saves
+// the flag's extra round trip.
+template <int RPW, int SW>
+__device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, float* dst, int gl, unsigned* err) {
   constexpr int NG = NGLUE * 64;
-  static_assert(NG * 2 >= G && NG * 2 >= MAX_ITEMS, "two flags per glue lane");
-  bool skip = false;
-  {
-    // both of this lane's flags in flight together; re-poll until current
-    const int i0 = gl, i1 = gl + NG;
-    unsigned f0 = i0 < nprod ? fload(flags + i0) : tag;
-    unsigned f1 = i1 < nprod ? fload(flags + i1) : tag;
-    unsigned spins = 0;
-    while (f0 != tag || f1 != tag) {
-      if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(err))) {
-        raise_err(err, 1u);
-        skip = true;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-      if (f0 != tag) f0 = fload(flags + i0);
-      if (f1 != tag) f1 = fload(flags + i1);
-    }
-  }
-  if (gl < 64) PK_TRACE(p, tidx, gl);
   for (int base = 0; base < n; base += MAXW * NG) {
     u64 w[MAXW];
 #pragma unroll
     for (int k = 0; k < MAXW; ++k) {
       const int i = base + gl + k * NG;
-      w[k] = (i < n && !skip) ? PK_G(u64, src)[i] : ((u64)tag << 32);
+      w[k] = i < n ? tload(src + slot_of<RPW, SW>(i)) : ((u64)tag << 32);
     }
     unsigned spins = 0;
     for (;;) {
@@ -449,7 +470,7 @@ __device__ __forceinline__ void glue_fetch(const unsigned* flags, int nprod, con
 #pragma unroll
       for (int k = 0; k < MAXW; ++k) {
         const int i = base + gl + k * NG;
-        if (i < n && (unsigned)(w[k] >> 32) != tag) w[k] = tload(src + i);
+        if (i < n && (unsigned)(w[k] >> 32) != tag) w[k] = tload(src + slot_of<RPW, SW>(i));
       }
     }
 #pragma unroll
@@ -500,6 +521,91 @@ __device__ __forceinline__ void leader_layernorm(const float* src, const LnParam
   for (int k = 0; k < NK; ++k) dst[lane + 64 * k] = (x[k] - mean) * inv_std * q.w[k] + q.b[k];
 }
 
+// ---------------------------------------------------------------------------
+// Attention of one item on the helper waves. Helper hw owns cached rows
+// [h0, h1) of the item's head and processes them in windows of KVW rows held
+// in its own part of the LDS stage.
+// ---------------------------------------------------------------------------
+constexpr int KVW = KVS / NA;  // rows of one helper's LDS window
+
+// Copy K/V rows [r0, r0 + n), n <= KVW, into a helper's LDS window with
+// LDS-direct loads (global_load_lds_dwordx4: lane i of an instruction fills
+// bytes [16i, 16i + 16) after the wave-uniform LDS address), so no registers
+// are held while the rows are in flight; the wave's own s_waitcnt vmcnt(0)
+// makes them readable by that wave. The last instruction repeats row
+// r0 + n - 1 into the unused rows of the window.
+__device__ __forceinline__ void stage_rows(const float* Kh, const float* Vh, int r0, int n, float* ldsK, float* ldsV,
+                                           int lane) {
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  const int off = (lane & 15) * 4;
+  for (int i = 0; 4 * i < n; ++i) {
+    const long row = min(r0 + 4 * i + (lane >> 4), r0 + n - 1);
+    __builtin_amdgcn_global_load_lds(PK_G(void, Kh + row * HD + off), (lds_ptr)(ldsK + 4 * i * HD), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(PK_G(void, Vh + row * HD + off), (lds_ptr)(ldsV + 4 * i * HD), 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0) only
+
+// Sum over the 16 lanes of one DPP row; every lane of the row gets the sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  return v;
+}
+
+// Online-softmax update of (m, lsum, o4) with the n rows (1 <= n <= KVW) of a
+// helper's LDS window (gpt2.rs:796-830: scores q.k / sqrt(64), softmax, p.V).
+// 16 lanes per row (4 dims each), 4 rows per wave instruction; lane (grp, dq)
+// accumulates lsum and o4 over rows 4t + grp, summed over grp by the caller.
+// AT row groups of 4 (n <= 4 * AT); straight-line code so that all LDS reads
+// of a loop are in flight together.
+template <int AT>
+__device__ __forceinline__ void att_window_t(const float* ldsK, const float* ldsV, int n, const float4& q4, int grp,
+                                             int dq, float& m, float& lsum, float4& o4) {
+  const float scale = 0.125f;  // 1 / sqrt(64)
+  float4 k[AT];
+#pragma unroll
+  for (int t = 0; t < AT; ++t) k[t] = *reinterpret_cast<const float4*>(ldsK + min(4 * t + grp, n - 1) * HD + dq);
+  float s[AT];
+  float mb = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < AT; ++t) {
+    const float dot = row16_sum(q4.x * k[t].x + q4.y * k[t].y + q4.z * k[t].z + q4.w * k[t].w);
+    s[t] = 4 * t + grp < n ? dot * scale : -INFINITY;
+    mb = fmaxf(mb, s[t]);
+  }
+  mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+  mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+  const float mn = fmaxf(m, mb);
+  const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+  lsum *= corr;
+  o4.x *= corr;
+  o4.y *= corr;
+  o4.z *= corr;
+  o4.w *= corr;
+#pragma unroll
+  for (int t = 0; t < AT; ++t) {
+    const float pj = s[t] == -INFINITY ? 0.f : expf(s[t] - mn);
+    const float4 v = *reinterpret_cast<const float4*>(ldsV + min(4 * t + grp, n - 1) * HD + dq);
+    lsum += pj;
+    o4.x += pj * v.x;
+    o4.y += pj * v.y;
+    o4.z += pj * v.z;
+    o4.w += pj * v.w;
+  }
+  m = mn;
+}
+__device__ __forceinline__ void att_window(const float* ldsK, const float* ldsV, int n, const float4& q4, int grp,
+                                           int dq, float& m, float& lsum, float4& o4) {
+  static_assert(KVW == 64, "window of 16 row groups");
+  if (n > 32) att_window_t<16>(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
+  else if (n > 16) att_window_t<8>(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
+  else att_window_t<4>(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
+}
+
 // Leader only: publish in_vec to the GEMV waves and wait for their partials.
 template <int D>
 __device__ __forceinline__ void leader_run_gemv(Smem<D>& sm, unsigned& seq, int lane, unsigned* err) {
@@ -547,10 +653,22 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   const int ih = item >= 0 ? item / NCH : 0, ic = item >= 0 ? item - ih * NCH : 0;
   const int CL = (len + NCH - 1) / NCH;
   const int j0 = ic * CL, j1 = min(len, j0 + CL);
+  // Helper rows: the cached rows [j0, min(j1, pos)) of the item are split
+  // between the helpers; the new row pos (when in the item) goes to the last
+  // helper. Cached rows are final at step start, so each helper loads its
+  // first window of a layer into LDS long before the layer's q is known.
+  const int hw = gw > 0 ? gw - 1 : 0;
+  const int cend = min(j1, pos), per = (cend - j0 + NA - 1) / NA;
+  const int h0 = min(cend, j0 + hw * per), h1 = min(cend, h0 + per);
+  const bool has_new = hw == NA - 1 && j1 == len;
+  float* ldsK = sm.kv_k + hw * KVW * HD;
+  float* ldsV = sm.kv_v + hw * KVW * HD;
+  const long kv_head = (long)ih * p.P * HD;
+  if (item >= 0 && !leader && h1 > h0)
+    stage_rows(p.kc + kv_head, p.vc + kv_head, h0, min(KVW, h1 - h0), ldsK, ldsV, lane);
   for (int l = 0; l < p.L; ++l) {
     const __attribute__((address_space(4))) LayerPtrs& LP = PK_C(LayerPtrs, p.layers)[l];
     u64* T = p.tag + (long)l * p.lw;
-    unsigned* FL = p.flags + (long)l * p.fl;
     // ---- QKV: LN1(x) @ c_attn + bias; k/v of the new token into the cache ----
     const int tb = 1 + 16 * l;  // trace index base of this layer
     // parameters of this phase, loaded before waiting for its input
@@ -562,13 +680,13 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       if (lane < rows_here) bias = PK_G(float, LP.bqkv)[row0 + lane];
     }
     if (l > 0) {
-      glue_fetch(p.flags + (long)(l - 1) * p.fl + F_X3, G, p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw,
-                 gl, p.err, p, -1);
+      glue_fetch<GM::RPW, GM::SW>(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
       glue_barrier(sm, gen, lane, p.err);
     }
     if (leader) {
       PK_TRACE(p, tb + 0, lane);
       leader_layernorm<D>(sm.xraw, lnq, p.eps, sm.in_vec[1], lane);
+      PK_TRACE(p, 803 + 4 * l, lane);
       leader_run_gemv(sm, seq, lane, p.err);
       PK_TRACE(p, tb + 1, lane);
       const int row0 = wg * GQ::RPW, rows_here = min(GQ::RPW, GQ::N - row0);
@@ -577,7 +695,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
         const float v = row_acc<GQ>(sm, lr) + bias;
-        tstore(T + p.o_qkv + n, v, tag);
+        tstore(T + p.o_qkv + wg * GQ::SW + lr, v, tag);
         if (n >= D) {
           const int c = n < 2 * D ? n - D : n - 2 * D;
           const int h = c / HD, dd = c - h * HD;
@@ -592,8 +710,10 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
     if (item >= 0) {
       if (leader) {
         // q, k_new, v_new of head ih: all three loads in flight, then re-poll
-        const u64* src = T + p.o_qkv + ih * HD + lane;
-        u64 wq = tload(src), wk = tload(src + D), wv = tload(src + 2 * D);
+        const u64* q = T + p.o_qkv + slot_of<GQ::RPW, GQ::SW>(ih * HD + lane);
+        const u64* k = T + p.o_qkv + slot_of<GQ::RPW, GQ::SW>(D + ih * HD + lane);
+        const u64* v = T + p.o_qkv + slot_of<GQ::RPW, GQ::SW>(2 * D + ih * HD + lane);
+        u64 wq = tload(q), wk = tload(k), wv = tload(v);
         unsigned spins = 0;
         while ((unsigned)(wq >> 32) != tag || (unsigned)(wk >> 32) != tag || (unsigned)(wv >> 32) != tag) {
           if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(p.err))) {
@@ -601,9 +721,9 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
             break;
           }
           __builtin_amdgcn_s_sleep(1);
-          if ((unsigned)(wq >> 32) != tag) wq = tload(src);
-          if ((unsigned)(wk >> 32) != tag) wk = tload(src + D);
-          if ((unsigned)(wv >> 32) != tag) wv = tload(src + 2 * D);
+          if ((unsigned)(wq >> 32) != tag) wq = tload(q);
+          if ((unsigned)(wk >> 32) != tag) wk = tload(k);
+          if ((unsigned)(wv >> 32) != tag) wv = tload(v);
         }
         sm.att_q[lane] = __uint_as_float((unsigned)wq);
         sm.att_k[lane] = __uint_as_float((unsigned)wk);
@@ -612,62 +732,37 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       }
       glue_barrier(sm, gen, lane, p.err);
       if (!leader) {
-        const int hw = gw - 1;
-        const int per = (j1 - j0 + NA - 1) / NA;
-        const int a0 = j0 + hw * per, a1 = min(j1, a0 + per);
-        const float* Kh = p.kc + (long)l * p.kv_layer + (long)ih * p.P * HD;
-        const float* Vh = p.vc + (long)l * p.kv_layer + (long)ih * p.P * HD;
-        // 16 lanes per position (4 dims each), 4 positions per row of the
-        // wave, AT positions-groups per block: all K and V rows of a block
-        // are loaded together, then an online-softmax update per block.
-        constexpr int AT = 8;
+        if (gw == 1) PK_TRACE(p, 801 + 4 * l, lane);
+        const float* Kh = p.kc + (long)l * p.kv_layer + kv_head;
+        const float* Vh = p.vc + (long)l * p.kv_layer + kv_head;
         const int grp = lane >> 4, dq = (lane & 15) * 4;
-        const float scale = 0.125f;  // 1 / sqrt(64)
         const float4 q4 = *reinterpret_cast<const float4*>(sm.att_q + dq);
         float m = -INFINITY, lsum = 0.f;
         float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int jb = a0; jb < a1; jb += 4 * AT) {
-          float4 k4[AT], v4[AT];
-#pragma unroll
-          for (int t = 0; t < AT; ++t) {
-            const int j = min(jb + 4 * t + grp, a1 - 1);
-            k4[t] = j == pos ? *reinterpret_cast<const float4*>(sm.att_k + dq) : ld4g(Kh + (long)j * HD + dq);
-            v4[t] = j == pos ? *reinterpret_cast<const float4*>(sm.att_v + dq) : ld4g(Vh + (long)j * HD + dq);
-          }
-          float s[AT];
-          float mb = -INFINITY;
-#pragma unroll
-          for (int t = 0; t < AT; ++t) {
-            float dot = q4.x * k4[t].x + q4.y * k4[t].y + q4.z * k4[t].z + q4.w * k4[t].w;
-            dot += dpp_mov<0xB1>(dot);  // sum over the 16 lanes of this position (one DPP row)
-            dot += dpp_mov<0x4E>(dot);
-            dot += dpp_mov<0x124>(dot);
-            dot += dpp_mov<0x128>(dot);
-            s[t] = (jb + 4 * t + grp < a1) ? dot * scale : -INFINITY;
-            mb = fmaxf(mb, s[t]);
-          }
-          mb = wmax(mb);
-          const float mn = fmaxf(m, mb);
+        for (int w0 = h0; w0 < h1; w0 += KVW) {
+          const int n = min(KVW, h1 - w0);
+          if (w0 > h0) stage_rows(Kh, Vh, w0, n, ldsK, ldsV, lane);  // windows after the first
+          wait_vm_all();
+          att_window(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
+        }
+        if (has_new) {  // row pos: k/v of the new token, counted once (row group 0)
+          const float4 k = *reinterpret_cast<const float4*>(sm.att_k + dq);
+          const float4 v = *reinterpret_cast<const float4*>(sm.att_v + dq);
+          const float s = row16_sum(q4.x * k.x + q4.y * k.y + q4.z * k.z + q4.w * k.w) * 0.125f;
+          const float mn = fmaxf(m, s);
           const float corr = m == -INFINITY ? 0.f : expf(m - mn);
-          lsum *= corr;
-          o4.x *= corr;
-          o4.y *= corr;
-          o4.z *= corr;
-          o4.w *= corr;
-#pragma unroll
-          for (int t = 0; t < AT; ++t) {
-            const float pj = s[t] == -INFINITY ? 0.f : expf(s[t] - mn);
-            if ((lane & 15) == 0) lsum += pj;
-            o4.x += pj * v4[t].x;
-            o4.y += pj * v4[t].y;
-            o4.z += pj * v4[t].z;
-            o4.w += pj * v4[t].w;
-          }
+          const float pj = grp == 0 ? expf(s - mn) : 0.f;
+          lsum = lsum * corr + pj;
+          o4.x = o4.x * corr + pj * v.x;
+          o4.y = o4.y * corr + pj * v.y;
+          o4.z = o4.z * corr + pj * v.z;
+          o4.w = o4.w * corr + pj * v.w;
           m = mn;
         }
-        lsum = wsum(lsum);
+        // sum over the 4 row groups
 #pragma unroll
         for (int o = 16; o < 64; o <<= 1) {
+          lsum += __shfl_xor(lsum, o, 64);
           o4.x += __shfl_xor(o4.x, o, 64);
           o4.y += __shfl_xor(o4.y, o, 64);
           o4.z += __shfl_xor(o4.z, o, 64);
@@ -680,11 +775,16 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
           sm.att_part[hw][2 + dq + 3] = o4.w;
         }
         if (lane == 0) {
-          sm.att_part[hw][0] = a1 > a0 ? m : -INFINITY;
-          sm.att_part[hw][1] = a1 > a0 ? lsum : 0.f;
+          sm.att_part[hw][0] = m;  // -inf (and lsum 0) when this helper had no rows
+          sm.att_part[hw][1] = lsum;
         }
+        if (gw == 1) PK_TRACE(p, 802 + 4 * l, lane);
       }
       glue_barrier(sm, gen, lane, p.err);
+      if (!leader && l + 1 < p.L && h1 > h0) {  // the window is free again: load the next layer's first one
+        const long nl = (long)(l + 1) * p.kv_layer + kv_head;
+        stage_rows(p.kc + nl, p.vc + nl, h0, min(KVW, h1 - h0), ldsK, ldsV, lane);
+      }
       if (leader) {  // merge the helpers' (m, l, o) into the item's partial softmax
         PK_TRACE(p, tb + 4, lane);
         float M = -INFINITY;
@@ -697,13 +797,12 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
           Ls += sm.att_part[w][1] * f;
           o += sm.att_part[w][2 + lane] * f;
         }
-        u64* dst = T + p.o_att + (long)item * ITEM_WORDS;
+        u64* dst = T + p.o_att + (long)item * ITEM_SLOT;
         tstore(dst + 2 + lane, o, tag);
         if (lane == 0) {
           tstore(dst, M, tag);
           tstore(dst + 1, Ls, tag);
         }
-        raise_flag(FL + F_ATT + item, tag, lane);
       }
     }
     // ---- attention projection + residual (gpt2.rs:523-526) ----
@@ -711,7 +810,8 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
       bias = lane < rows_here ? PK_G(float, LP.baproj)[row0 + lane] : 0.f;
     }
-    glue_fetch(FL + F_ATT, items, T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err, p, tb + 14);
+    glue_fetch<ITEM_WORDS, ITEM_SLOT>(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
+    if (leader) PK_TRACE(p, tb + 14, lane);
     glue_barrier(sm, gen, lane, p.err);
     // merge the chunks of each head; heads are spread over the glue waves
     for (int h = gw; h < H; h += NGLUE) {
@@ -735,9 +835,8 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
-        tstore(T + p.o_x2 + n, sm.xraw[n] + (row_acc<GP>(sm, lr) + bias), tag);
+        tstore(T + p.o_x2 + wg * GP::SW + lr, sm.xraw[n] + (row_acc<GP>(sm, lr) + bias), tag);
       }
-      raise_flag(FL + F_X2 + wg, tag, lane);
       PK_TRACE(p, tb + 7, lane);
     }
     // ---- FC + gelu_new (gpt2.rs:529-533) ----
@@ -746,7 +845,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int row0 = wg * GF::RPW, rows_here = min(GF::RPW, GF::N - row0);
       bias = lane < rows_here ? PK_G(float, LP.bfc)[row0 + lane] : 0.f;
     }
-    glue_fetch(FL + F_X2, G, T + p.o_x2, D, tag, sm.x2raw, gl, p.err, p, -1);
+    glue_fetch<GP::RPW, GP::SW>(T + p.o_x2, D, tag, sm.x2raw, gl, p.err);
     glue_barrier(sm, gen, lane, p.err);
     if (leader) {
       PK_TRACE(p, tb + 8, lane);
@@ -756,9 +855,8 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int row0 = wg * GF::RPW, rows_here = min(GF::RPW, GF::N - row0);
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
-        tstore(T + p.o_h + n, gelu_new(row_acc<GF>(sm, lr) + bias), tag);
+        tstore(T + p.o_h + wg * GF::SW + lr, gelu_new(row_acc<GF>(sm, lr) + bias), tag);
       }
-      raise_flag(FL + F_H + wg, tag, lane);
       PK_TRACE(p, tb + 10, lane);
     }
     // ---- MLP projection + residual (gpt2.rs:534-537) ----
@@ -766,7 +864,8 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int row0 = wg * GM::RPW, rows_here = min(GM::RPW, GM::N - row0);
       bias = lane < rows_here ? PK_G(float, LP.bmproj)[row0 + lane] : 0.f;
     }
-    glue_fetch(FL + F_H, G, T + p.o_h, 4 * D, tag, sm.in_vec[0], gl, p.err, p, tb + 15);
+    glue_fetch<GF::RPW, GF::SW>(T + p.o_h, 4 * D, tag, sm.in_vec[0], gl, p.err);
+    if (leader) PK_TRACE(p, tb + 15, lane);
     glue_barrier(sm, gen, lane, p.err);
     if (leader) {
       PK_TRACE(p, tb + 11, lane);
@@ -775,17 +874,15 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int row0 = wg * GM::RPW, rows_here = min(GM::RPW, GM::N - row0);
       for (int lr = lane; lr < rows_here; lr += 64) {
         const int n = row0 + lr;
-        tstore(T + p.o_x3 + n, sm.x2raw[n] + (row_acc<GM>(sm, lr) + bias), tag);
+        tstore(T + p.o_x3 + wg * GM::SW + lr, sm.x2raw[n] + (row_acc<GM>(sm, lr) + bias), tag);
       }
-      raise_flag(FL + F_X3 + wg, tag, lane);
       PK_TRACE(p, tb + 13, lane);
     }
   }
   // ---- ln_f + tied LM head + argmax (gpt2.rs:392-396, 858-868) ----
   LnParams<D> lnf;
   if (leader) ln_prefetch<D>(lnf, p.lnfw, p.lnfb, lane);
-  glue_fetch(p.flags + (long)(p.L - 1) * p.fl + F_X3, G, p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw,
-             gl, p.err, p, 4 + 16 * p.L);
+  glue_fetch<GM::RPW, GM::SW>(p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
   glue_barrier(sm, gen, lane, p.err);
   if (leader) {
     PK_TRACE(p, 1 + 16 * p.L, lane);
@@ -817,13 +914,15 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   }
 }
 
-// Attention chunking for this step: NCH chunks per head (>= 32 positions
-// each, at most CMAX and H*NCH <= min(MAX_ITEMS, G)).
+// Attention chunking for this step: NCH chunks per head, one per KVS
+// positions (so each chunk fits the LDS stage), at most CMAX and
+// H*NCH <= min(MAX_ITEMS, G). Fewer chunks keep the exchange that every
+// workgroup reads (H*NCH partial softmax items) small.
 template <int H>
 __device__ __host__ __forceinline__ int att_chunks(int len) {
   constexpr int cap0 = CMAX < MAX_ITEMS / H ? CMAX : MAX_ITEMS / H;
   constexpr int cap = cap0 < G / H ? cap0 : G / H;
-  int c = (len + 31) / 32;
+  int c = (len + KVS - 1) / KVS;
   c = c < cap ? c : cap;
   return c < 1 ? 1 : c;
 }
@@ -837,13 +936,23 @@ __global__ __launch_bounds__(NTHREADS) void decode_step_kernel(Params p) {
     sm.gemv_ready = 0;
     sm.gemv_done = 0;
     sm.glue_cnt = 0;
+    sm.trace_t0 = wall_clock64();
   }
+  if (p.trace)
+    for (int i = threadIdx.x; i < TRACE_N; i += NTHREADS) sm.trace_rel[i] = 0;
   __syncthreads();
   const int len = *PK_G(int, p.pos) + 1;
   const unsigned tag = *PK_G(unsigned, p.epoch);
   const int nch = att_chunks<C::H>(len);
   if (wave < NGLUE) glue_role<C>(p, sm, wave, lane, len, nch, C::H * nch, tag);
   else gemv_role<C>(p, sm, wave - NGLUE, lane);
+  if (p.trace) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < TRACE_N; i += NTHREADS) {
+      const unsigned r = sm.trace_rel[i];
+      PK_GW(u64, p.trace)[(long)blockIdx.x * TRACE_STRIDE + i] = r ? sm.trace_t0 + r : 0ull;
+    }
+  }
 }
 
 }  // namespace pk
