@@ -68,6 +68,41 @@ def cpu_baseline(sd, sh, prompt, n_decode):
             "prefill_tok_s": len(prompt) / (t1 - t0)}
 
 
+def measured_traffic(workload):
+    """HBM bytes per decode_step_kernel launch measured by the rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (scaled by the
+    copy-kernel calibration recorded there); None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", f"decode_step_kernel_{workload}_hbm_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def calib_copy(nbytes):
+    """One hipMemset (a fill kernel writing nbytes) and one device-to-device
+    hipMemcpy (the runtime's copy kernel: reads and writes nbytes), so that a
+    rocprofv3 --pmc pass over this run can scale FETCH_SIZE / WRITE_SIZE."""
+    import ctypes as C
+    try:
+        hip = C.CDLL("libamdhip64.so")
+    except OSError:
+        hip = C.CDLL("/opt/rocm/lib/libamdhip64.so")
+    src, dst = C.c_void_p(), C.c_void_p()
+    n = C.c_size_t(nbytes)
+    ok = hip.hipMalloc(C.byref(src), n) == 0 and hip.hipMalloc(C.byref(dst), n) == 0
+    ok = ok and hip.hipMemset(src, 1, n) == 0 and hip.hipDeviceSynchronize() == 0
+    ok = ok and hip.hipMemcpy(dst, src, n, 3) == 0 and hip.hipDeviceSynchronize() == 0  # 3: device to device
+    for p in (src, dst):
+        if p.value:
+            hip.hipFree(p)
+    if not ok:
+        raise RuntimeError("calibration copy failed")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -76,6 +111,9 @@ def main():
     ap.add_argument("--workload", default="c1", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-decode-steps", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one device-to-device copy of 256 MiB (untimed): the reference kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -93,6 +131,8 @@ def main():
     cfg = Gpt2Config(sh.vocab_size, sh.n_positions, sh.n_embd, sh.n_layer, sh.n_head, sh.layer_norm_epsilon)
     m = Gpt2Model.from_state_dict(sd, cfg, storage=storage)
     prompts = np.stack([synth.make_tokens(n_prompt, sh.vocab_size, stream=b) for b in range(B)])
+    if a.calib_copy:
+        calib_copy(256 << 20)
     print("[bench] model resident; warming up", file=sys.stderr, flush=True)
     for _ in range(a.warmup):
         m.generate_cached_batched(prompts, n_new)
@@ -124,6 +164,7 @@ def main():
         kernel = "decode step (graph of per-op kernels)"
         dur_ms = step_ms
     achieved = avg_bytes / (dur_ms / 1e3) / 1e9
+    traffic = measured_traffic(a.workload) if kern_n else None
     out = {
         "metric": METRIC,
         "value": round(dec_tok_s, 2),
@@ -143,7 +184,7 @@ def main():
         "decode_ms_per_token_step": round(step_ms, 4),
         "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "bytes_per_launch": int(avg_bytes), "avg_launch_ms": round(dur_ms, 5), "traffic": None},
+                     "bytes_per_launch": int(avg_bytes), "avg_launch_ms": round(dur_ms, 5), "traffic": traffic},
         "first_ids": ids[0, n_prompt:n_prompt + 8].tolist(),
     }
     if not a.no_cpu and a.workload == "c1":
