@@ -46,7 +46,7 @@ constexpr int HD = 64;              // head_dim of every GPT-2 size
 constexpr int CMAX = 16;            // attention chunks per head
 constexpr int ITEM_WORDS = 2 + HD;  // m, l, o[64]
 constexpr int MAX_ITEMS = 64;       // heads * chunks merged by the consumers
-constexpr int MAXW = 16;            // polled words per glue lane per round
+constexpr int MAXW = 8;             // polled words per glue lane per round (16 spills registers)
 constexpr int PART_MAX = 1536;      // segment partials per workgroup
 constexpr int KVS = 128;            // cached positions of one item staged in LDS
 // Exchange layout: each producer owns a slot of whole 128-byte lines, so no
@@ -600,10 +600,13 @@ __device__ __forceinline__ void att_window_t(const float* ldsK, const float* lds
 }
 __device__ __forceinline__ void att_window(const float* ldsK, const float* ldsV, int n, const float4& q4, int grp,
                                            int dq, float& m, float& lsum, float4& o4) {
-  static_assert(KVW == 64, "window of 16 row groups");
-  if (n > 32) att_window_t<16>(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
-  else if (n > 16) att_window_t<8>(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
-  else att_window_t<4>(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
+  // blocks of at most 32 rows (8 row groups) keep the registers of one block
+  // small; a partial block uses 4 groups when it has at most 16 rows
+  for (int b0 = 0; b0 < n; b0 += 32) {
+    const int nb = min(32, n - b0);
+    if (nb > 16) att_window_t<8>(ldsK + b0 * HD, ldsV + b0 * HD, nb, q4, grp, dq, m, lsum, o4);
+    else att_window_t<4>(ldsK + b0 * HD, ldsV + b0 * HD, nb, q4, grp, dq, m, lsum, o4);
+  }
 }
 
 // Leader only: publish in_vec to the GEMV waves and wait for their partials.
