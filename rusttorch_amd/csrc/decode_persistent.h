@@ -31,10 +31,12 @@ void persistent_plan_destroy(PersistentPlan* p);
 bool persistent_supported(const PersistentPlan* p, int batch);
 PersistentState* persistent_state_create(PersistentPlan* p, float* kcache, float* vcache, int batch,
                                          uint32_t* token_dev, int* pos_dev, float* logits,
-                                         unsigned long long* keys);
+                                         unsigned long long* keys, uint32_t* ids_dev, int* step_dev);
 void persistent_state_destroy(PersistentState* s);
-// Enqueue one decode step (reads *token_dev / *pos_dev, writes logits and the
-// packed argmax key). The caller's finalize kernel must advance *epoch.
+// Enqueue one decode step: reads *token_dev / *pos_dev, writes the logits,
+// and finishes the step itself (the finalize kernel's work): the argmax token
+// goes to *token_dev and ids_dev[*step_dev], *pos_dev and *step_dev advance
+// by one, the packed argmax key is cleared.
 hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative);
 unsigned* persistent_epoch(PersistentState* s);
 unsigned* persistent_err(PersistentState* s);

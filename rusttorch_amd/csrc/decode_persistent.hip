@@ -53,6 +53,7 @@ struct PersistentState {
   unsigned* epoch = nullptr;
   unsigned* err = nullptr;
   pk::u64* trace = nullptr;
+  unsigned* done = nullptr;
 };
 
 PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
@@ -117,7 +118,7 @@ bool persistent_supported(const PersistentPlan* pl, int batch) {
 
 PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, float* vcache, int batch,
                                          uint32_t* token_dev, int* pos_dev, float* logits,
-                                         unsigned long long* keys) {
+                                         unsigned long long* keys, uint32_t* ids_dev, int* step_dev) {
   if (!persistent_supported(pl, batch)) return nullptr;
   PersistentState* s = new PersistentState();
   s->plan = pl;
@@ -125,12 +126,13 @@ PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, floa
   pk::Params& p = s->p;
   const size_t words = (size_t)p.lw * p.L;
   if (hipMalloc(&s->tags, words * 8) != hipSuccess || hipMalloc(&s->epoch, 256) != hipSuccess ||
-      hipMalloc(&s->err, 256) != hipSuccess) {
+      hipMalloc(&s->err, 256) != hipSuccess || hipMalloc(&s->done, 256) != hipSuccess) {
     persistent_state_destroy(s);
     return nullptr;
   }
   // tag 0 never matches: the epoch starts at 1 and only grows
-  if (hipMemset(s->tags, 0, words * 8) != hipSuccess || hipMemset(s->err, 0, 256) != hipSuccess) {
+  if (hipMemset(s->tags, 0, words * 8) != hipSuccess || hipMemset(s->err, 0, 256) != hipSuccess ||
+      hipMemset(s->done, 0, 256) != hipSuccess) {
     persistent_state_destroy(s);
     return nullptr;
   }
@@ -155,6 +157,9 @@ PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, floa
   p.pos = pos_dev;
   p.logits = logits;
   p.keys = keys;
+  p.ids_out = ids_dev;
+  p.step = step_dev;
+  p.done = s->done;
   return s;
 }
 
@@ -164,6 +169,7 @@ void persistent_state_destroy(PersistentState* s) {
   if (s->epoch) hipFree(s->epoch);
   if (s->err) hipFree(s->err);
   if (s->trace) hipFree(s->trace);
+  if (s->done) hipFree(s->done);
   delete s;
 }
 

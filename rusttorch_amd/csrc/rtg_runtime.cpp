@@ -279,8 +279,8 @@ static void enqueue_decode_step(rtg_cache* c) {
     launch_gemv(s, B, m->wte, m->wtype, nullptr, c->ln, d, c->logits, V, V, d, EPI_NONE);
     launch_argmax(s, c->logits, V, B, V, c->keys);
   }
-  launch_finalize(s, B, c->keys, c->token_dev, c->ids_dev, P, c->pos_dev, c->step_dev,
-                  c->pstate ? persistent_epoch(c->pstate) : nullptr);
+  if (!c->pstate)  // the persistent step finishes itself
+    launch_finalize(s, B, c->keys, c->token_dev, c->ids_dev, P, c->pos_dev, c->step_dev, nullptr);
 }
 
 static void set_counters(rtg_cache* c, int pos, int step) {
@@ -373,7 +373,8 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   ensure_logits(c, B * n);
   hipStream_t s = c->stream;
   if (!c->pstate && persistent_supported(m->pplan, (int)B)) {
-    c->pstate = persistent_state_create(m->pplan, c->k, c->v, (int)B, c->token_dev, c->pos_dev, c->logits, c->keys);
+    c->pstate = persistent_state_create(m->pplan, c->k, c->v, (int)B, c->token_dev, c->pos_dev, c->logits, c->keys,
+                                        c->ids_dev, c->step_dev);
     destroy_graph(c);  // the step graph changes shape
   }
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
@@ -403,8 +404,6 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
       HIPX(hipEventRecord(evs[2 * (i - 1)], s));
       HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/true));
       HIPX(hipEventRecord(evs[2 * (i - 1) + 1], s));
-      launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev,
-                      persistent_epoch(c->pstate));
     }
     HIPX(hipStreamSynchronize(s));
     for (size_t i = 0; i + 1 < evs.size(); i += 2) {
