@@ -68,6 +68,66 @@ def cpu_baseline(sd, sh, prompt, n_decode):
             "prefill_tok_s": len(prompt) / (t1 - t0)}
 
 
+MFMA_FP32_PEAK_TFLOPS = 157.3
+PREFILL_WORKLOADS = {
+    # name: (shape, batch, tokens): forward_cached on an empty cache, full [T, V] logits per sequence
+    "c4": ("large", 32, 1024),
+}
+
+
+def prefill_flops(sh, B, T):
+    """Algorithmic flops of forward_cached over T new tokens on an empty
+    cache: the four Conv1D GEMMs, causal QK^T and PV, and the LM head over
+    every row (the reference computes [T, V] logits)."""
+    L, d, V = sh.n_layer, sh.n_embd, sh.vocab_size
+    return B * (2 * T * 12 * d * d * L + 4 * d * L * T * (T + 1) // 2 + 2 * T * d * V)
+
+
+def run_prefill(a):
+    from rusttorch_amd import synth
+    from rusttorch_amd.gpt2 import Gpt2Config, Gpt2Model
+
+    shape_name, B, T = PREFILL_WORKLOADS[a.workload]
+    sh = synth.SHAPES[shape_name]
+    sd = synth.make_weights(sh)
+    cfg = Gpt2Config(sh.vocab_size, sh.n_positions, sh.n_embd, sh.n_layer, sh.n_head, sh.layer_norm_epsilon)
+    m = Gpt2Model.from_state_dict(sd, cfg)
+    del sd
+    ids = np.stack([synth.make_tokens(T, sh.vocab_size, stream=b) for b in range(B)])
+    cache = m.new_cache(B)
+    print("[bench] model resident; warming up", file=sys.stderr, flush=True)
+    for _ in range(a.warmup):
+        cache.clear()
+        m.forward_cached_batched(ids, cache, want_logits=False)
+    times = []
+    for _ in range(a.steps):
+        cache.clear()
+        t0 = time.perf_counter()
+        m.forward_cached_batched(ids, cache, want_logits=False)  # logits stay in HBM
+        times.append(time.perf_counter() - t0)
+    print("[bench] timed steps done", file=sys.stderr, flush=True)
+    step_s = float(np.mean(times))
+    flops = prefill_flops(sh, B, T)
+    achieved = flops / step_s / 1e12
+    out = {
+        "metric": f"prefill tokens/s (GPT-2 {shape_name} b={B}, {T} tokens)",
+        "value": round(B * T / step_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(step_s * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded N(0,0.02) random-init weights, uniform random token ids",
+        "config": {"workload": f"{a.workload}: GPT-2 {shape_name}, batch {B}, prefill {T} tokens, full logits",
+                   "batch": B, "tokens": T, "weights": "f32"},
+        "roofline": {"bound": "mfma", "kernel": "whole prefill (gemm_kernel dominant)",
+                     "achieved": round(achieved, 2), "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), "flops_per_step": flops,
+                     "traffic": None},
+    }
+    print(json.dumps(out))
+
+
 def measured_traffic(workload):
     """HBM bytes per decode_step_kernel launch measured by the rocprofv3
     FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (scaled by the
@@ -108,7 +168,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="c1", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c1", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
     ap.add_argument("--cpu-decode-steps", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
@@ -119,6 +179,10 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
               "sharding is described in DESIGN.md, not run", file=sys.stderr)
         sys.exit(2)
+
+    if a.workload in PREFILL_WORKLOADS:
+        run_prefill(a)
+        return
 
     from rusttorch_amd import synth
     from rusttorch_amd.gpt2 import Gpt2Config, Gpt2Model

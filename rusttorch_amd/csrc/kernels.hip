@@ -650,8 +650,168 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill causal attention for head_dim 64 on fp32 MFMA (flash-attention
+// form of multi_head_attention_cached, gpt2.rs:772-834). A workgroup of 4
+// waves takes 128 queries of one (sequence, head); each wave owns 32. Key
+// blocks of 32 rows are staged in LDS (K row-major, V transposed), the next
+// block's rows are loaded into registers while the current one is used.
+//
+// Per key block a wave computes S^T = K Q^T (32 keys x 32 queries, 32
+// v_mfma_f32_32x32x2f32 steps over the 64 dims: step kk pairs dims kk and
+// kk + 32), so accumulator i of lane l holds the score of query l % 32 with
+// key r(i, l) = (i/4)*8 + (l/32)*4 + i%4. The softmax statistics of a query
+// are therefore lane-local (16 values) plus one exchange between the two
+// lane halves, and the rescale of the output is lane-local.
+// O^T += V^T P^T runs 16 steps per 32-dim output tile; step kk takes key
+// r(kk, l) in lane half l/32, which is exactly accumulator kk of the lane,
+// so P feeds the MFMA from registers. Online softmax with running max m and
+// per-half partial sums l (combined at the end), as the scalar kernel.
+// ---------------------------------------------------------------------------
+
+constexpr int FA_QW = 32;         // queries per wave
+constexpr int FA_W = 4;           // waves per workgroup
+constexpr int FA_K = 32;          // keys per block
+constexpr int FA_KP = 64 + 4;     // padded K row (floats)
+constexpr int FA_VP = FA_K + 4;   // padded V^T row (floats)
+
+__global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
+    const float* __restrict__ qkv, int T, int past, const float* __restrict__ kc, const float* __restrict__ vc,
+    int H, int P, int d, int nqb, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float Ks[FA_K][FA_KP];
+  __shared__ __attribute__((aligned(16))) float Vt[64][FA_VP];
+  const int qb = nqb - 1 - (int)blockIdx.x;  // the longest (last) query blocks first
+  const int h = blockIdx.y, sidx = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 31, hh = lane >> 5;
+  const int qi = qb * FA_QW * FA_W + wave * FA_QW + c;  // this lane's query (0..T-1 when valid)
+  const bool qvalid = qi < T;
+  const int qpos = past + qi;
+  const size_t head_off = ((size_t)sidx * H + h) * (size_t)P * 64;
+  const float* Kh = kc + head_off;
+  const float* Vh = vc + head_off;
+  // this lane's half of its query row: dims [32*hh, 32*hh + 32)
+  float q[32];
+  {
+    const float* qrow = qkv + ((size_t)sidx * T + min(qi, T - 1)) * 3 * d + h * 64 + 32 * hh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 v = reinterpret_cast<const float4*>(qrow)[j];
+      q[4 * j] = v.x;
+      q[4 * j + 1] = v.y;
+      q[4 * j + 2] = v.z;
+      q[4 * j + 3] = v.w;
+    }
+  }
+  const int kmax = past + min(T, (qb + 1) * FA_QW * FA_W) - 1;  // last key any query here attends
+  const int nkb = kmax / FA_K + 1;
+  // staging: 512 float4 of K and of V per block, 2 each per thread
+  float4 kr[2], vr[2];
+  auto load_block = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + u * FA_QW * 2 * FA_W;
+      const int r = e >> 4, c4 = (e & 15) * 4, j = kb * FA_K + r;
+      const bool ok = j <= kmax;
+      kr[u] = ok ? *reinterpret_cast<const float4*>(Kh + (size_t)j * 64 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[u] = ok ? *reinterpret_cast<const float4*>(Vh + (size_t)j * 64 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  float m = -INFINITY, l = 0.f;
+  floatx16 o0, o1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    o0[i] = 0.f;
+    o1[i] = 0.f;
+  }
+  load_block(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();  // every wave is done with the previous block
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + u * FA_QW * 2 * FA_W;
+      const int r = e >> 4, c4 = (e & 15) * 4;
+      *reinterpret_cast<float4*>(&Ks[r][c4]) = kr[u];
+      Vt[c4][r] = vr[u].x;
+      Vt[c4 + 1][r] = vr[u].y;
+      Vt[c4 + 2][r] = vr[u].z;
+      Vt[c4 + 3][r] = vr[u].w;
+    }
+    __syncthreads();
+    if (kb + 1 < nkb) load_block(kb + 1);
+    // S^T = K Q^T
+    floatx16 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 a = *reinterpret_cast<const float4*>(&Ks[c][32 * hh + 4 * j]);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, q[4 * j], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, q[4 * j + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, q[4 * j + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, q[4 * j + 3], s, 0, 0, 0);
+    }
+    // causal mask (key j <= query position), scale 1/sqrt(64), online softmax
+    const int j0 = kb * FA_K;
+    float bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int j = j0 + (i / 4) * 8 + hh * 4 + (i % 4);
+      s[i] = j <= qpos ? s[i] * 0.125f : -INFINITY;
+      bm = fmaxf(bm, s[i]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[i] = s[i] == -INFINITY ? 0.f : expf(s[i] - mn);
+      ps += s[i];
+    }
+    l = l * corr + ps;
+    m = mn;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      o0[i] *= corr;
+      o1[i] *= corr;
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 v0 = *reinterpret_cast<const float4*>(&Vt[c][8 * g + 4 * hh]);
+      const float4 v1 = *reinterpret_cast<const float4*>(&Vt[32 + c][8 * g + 4 * hh]);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.x, s[4 * g], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.x, s[4 * g], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.y, s[4 * g + 1], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.y, s[4 * g + 1], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.z, s[4 * g + 2], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.z, s[4 * g + 2], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.w, s[4 * g + 3], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.w, s[4 * g + 3], o1, 0, 0, 0);
+    }
+  }
+  l += __shfl_xor(l, 32, 64);
+  if (qvalid) {
+    const float inv = 1.0f / l;
+    float* orow = out + ((size_t)sidx * T + qi) * d + h * 64;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = (i / 4) * 8 + hh * 4 + (i % 4);
+      orow[r] = o0[i] * inv;
+      orow[32 + r] = o1[i] * inv;
+    }
+  }
+}
+
 void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past, const float* kc, const float* vc,
                          int n_head, int n_pos, int d, float* out) {
+  if (d / n_head == 64) {
+    const int nqb = (T + FA_QW * FA_W - 1) / (FA_QW * FA_W);
+    dim3 grid(nqb, n_head, S);
+    attn_prefill_mfma_kernel<<<grid, FA_QW * 2 * FA_W, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
+    return;
+  }
   dim3 grid((T + PQ - 1) / PQ, n_head, S);
   attn_prefill_kernel<<<grid, PQ, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, d / n_head, out);
 }

@@ -211,6 +211,24 @@ def test_small_batched_matches_single(O):
         assert om.generate_cached(prompts[b], 12) == out[b, : n + 12].tolist()
 
 
+def test_long_prefill_attention_blocks(O):
+    """Prefill attention over many key blocks, several query blocks, a past
+    length that is not a block multiple and a second chunk appended to a
+    non-empty cache (gpt2.rs:772-834 with t > 0 and new_len > 1)."""
+    sd, sh, m = gpu_model("small")
+    B, n1, n2 = 2, 200, 150
+    ids = np.stack([synth.make_tokens(n1 + n2, sh.vocab_size, stream=300 + b) for b in range(B)])
+    c = m.new_cache(batch=B)
+    lg1 = m.forward_cached_batched(ids[:, :n1], c)
+    lg2 = m.forward_cached_batched(ids[:, n1:], c)
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    for b in range(B):
+        print(f"[gpu] long prefill oracle seq {b}", flush=True)
+        oc = om.new_cache()
+        assert_logits_close(lg1[b], om.forward_cached(ids[b, :n1], oc), f"first chunk seq {b}")
+        assert_logits_close(lg2[b], om.forward_cached(ids[b, n1:], oc), f"second chunk seq {b}")
+
+
 def test_batched_forward_logits(O):
     sd, sh, m = gpu_model("mini")
     B, n = 3, 10
