@@ -542,8 +542,97 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
   }
 }
 
+// Skinny GEMM for few rows (a short prompt): the 128x128 tile kernel would
+// launch only N/128 workgroups. Here a workgroup computes a 32x32 output tile
+// and each of its 4 waves a quarter of K. Step e of a wave's MFMA chain pairs
+// k = k0 + e (lanes 0-31) with k = k0 + KH + e (lanes 32-63), KH = half the
+// wave's K range, so each lane reads two contiguous runs (row m of A from L2,
+// row n of W streamed from HBM) as 16-byte vectors. The four partial tiles
+// are summed in LDS in wave order; then the tile kernel's epilogues.
+// Needs K % 64 == 0 (every GPT-2 width).
+constexpr int SK_CHUNK = 8;  // k per lane-run per loop step
+
+template <int WT>
+__device__ __forceinline__ void load8(const void* W, size_t idx, float* out) {
+  if (WT == W_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + idx);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + idx + 4);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(W) + idx);
+    out[0] = __uint_as_float(u.x << 16); out[1] = __uint_as_float(u.x & 0xffff0000u);
+    out[2] = __uint_as_float(u.y << 16); out[3] = __uint_as_float(u.y & 0xffff0000u);
+    out[4] = __uint_as_float(u.z << 16); out[5] = __uint_as_float(u.z & 0xffff0000u);
+    out[6] = __uint_as_float(u.w << 16); out[7] = __uint_as_float(u.w & 0xffff0000u);
+  }
+}
+
+template <int WT>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(const float* __restrict__ A, int lda,
+                                                          const void* __restrict__ W, const float* __restrict__ bias,
+                                                          float* __restrict__ C, long ldc, int M, int N, int K,
+                                                          int epi) {
+  __shared__ float red[4][32][33];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 31, hh = lane >> 5;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+  const int KW = K / 4, KH = KW / 2;
+  const int k0 = wave * KW + hh * KH;  // this lane's run: [k0, k0 + KH)
+  const float* arow = A + (size_t)min(m0 + r, M - 1) * lda + k0;
+  const size_t wrow = (size_t)min(n0 + r, N - 1) * K + k0;
+  floatx16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  // SK_DEPTH chunks in flight: chunk c lives in slot c % SK_DEPTH
+  constexpr int SK_DEPTH = 4;
+  const int nch = KH / SK_CHUNK;
+  float a[SK_DEPTH][SK_CHUNK], w[SK_DEPTH][SK_CHUNK];
+#pragma unroll
+  for (int d = 0; d < SK_DEPTH; ++d) {
+    const int k = min(d, nch - 1) * SK_CHUNK;
+    load8<W_F32>(arow, k, a[d]);
+    load8<WT>(W, wrow + k, w[d]);
+  }
+  for (int c0 = 0; c0 < nch; c0 += SK_DEPTH) {
+#pragma unroll
+    for (int d = 0; d < SK_DEPTH; ++d) {
+      if (c0 + d < nch) {
+#pragma unroll
+        for (int e = 0; e < SK_CHUNK; ++e)
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d][e], w[d][e], acc, 0, 0, 0);
+      }
+      const int kn = min(c0 + d + SK_DEPTH, nch - 1) * SK_CHUNK;  // refill (a repeat past the end)
+      load8<W_F32>(arow, kn, a[d]);
+      load8<WT>(W, wrow + kn, w[d]);
+    }
+  }
+  // lane holds the wave's partial of C[m0 + (i/4)*8 + hh*4 + i%4][n0 + r]
+#pragma unroll
+  for (int i = 0; i < 16; ++i) red[wave][(i >> 2) * 8 + hh * 4 + (i & 3)][r] = acc[i];
+  __syncthreads();
+  for (int idx = tid; idx < 32 * 32; idx += 256) {
+    const int mi = idx >> 5, ni = idx & 31;
+    const int m = m0 + mi, n = n0 + ni;
+    if (m >= M || n >= N) continue;
+    const float v = ((red[0][mi][ni] + red[1][mi][ni]) + red[2][mi][ni]) + red[3][mi][ni];
+    const float bv = bias ? bias[n] : 0.f;
+    float* cp = C + (size_t)m * ldc + n;
+    if (epi == EPI_BIAS) *cp = v + bv;
+    else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
+    else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
+    else *cp = v;
+  }
+}
+
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
                  long ldc, int M, int N, int K, int epi) {
+  if (M <= 64 && K % 64 == 0 && lda % 4 == 0) {
+    dim3 grid((N + 31) / 32, (M + 31) / 32);
+    if (wtype == W_F32) gemm_skinny_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
+    else gemm_skinny_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
+    return;
+  }
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
   if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
   else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
