@@ -147,6 +147,22 @@ struct GemvOut {
   const int* pos_dev;
 };
 
+// QKV epilogue of a decode step (q != nullptr): columns [0, d) are q, written
+// to q[m][n]; [d, 3d) are the new token's k / v of sequence m, written into
+// the cache at position *pos_dev (LayerKVCache::append, gpt2.rs:500-514).
+struct SkinnyQkv {
+  float* q;
+  int ldq;
+  int d;
+  KvDst kv;
+  const int* pos_dev;
+};
+
+// Skinny MFMA GEMM (defined with the prefill GEMM below); false when the
+// shape does not suit it.
+static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias,
+                          float* C, long ldc, int M, int N, int K, int epi, const SkinnyQkv& qkv);
+
 template <int BM, int WT, int R>
 __global__ __launch_bounds__(256) void gemv_kernel(const void* __restrict__ W, const float* __restrict__ bias,
                                                    const float* __restrict__ x, int ldx, int nb, int N, int K,
@@ -252,6 +268,8 @@ static void gemv_dispatch_b(hipStream_t s, int nb, const void* W, const float* b
 
 void launch_gemv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
                  float* y, int ldy, int N, int K, int epi) {
+  // several sequences: MFMA reads each weight once for all of them
+  if (B >= 2 && launch_skinny(s, x, ldx, W, wtype, bias, y, ldy, B, N, K, epi, SkinnyQkv{})) return;
   GemvOut o{};
   o.y = y; o.ldy = ldy; o.epi = epi;
   if (wtype == W_F32) gemv_dispatch_b<W_F32>(s, B, W, bias, x, ldx, N, K, o);
@@ -260,6 +278,9 @@ void launch_gemv(hipStream_t s, int B, const void* W, int wtype, const float* bi
 
 void launch_gemv_qkv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
                      float* q, int ldq, int d, KvDst kv, const int* pos_dev) {
+  if (B >= 2 && launch_skinny(s, x, ldx, W, wtype, bias, nullptr, 0, B, 3 * d, d, EPI_BIAS,
+                              SkinnyQkv{q, ldq, d, kv, pos_dev}))
+    return;
   GemvOut o{};
   o.q = q; o.ldq = ldq; o.d = d; o.kv = kv; o.pos_dev = pos_dev;
   if (wtype == W_F32) gemv_dispatch_b<W_F32>(s, B, W, bias, x, ldx, 3 * d, d, o);
@@ -316,10 +337,146 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
   if (tid < hd) out[(size_t)b * ldo + h * hd + tid] = (pv[tid] + pv[64 + tid]) + (pv[128 + tid] + pv[192 + tid]);
 }
 
+// Decode attention for head_dim 64, split over positions (one new token per
+// sequence, gpt2.rs:772-834): block (h, b, sp) takes positions
+// [128 sp, 128 sp + 128), 32 per wave; 16 lanes per position (4 dims each)
+// with the 16-lane sums in DPP, all K/V rows of a wave loaded at once. Each
+// block writes its partial softmax (m, l, o[64]); the combine kernel merges
+// the partials of the splits that exist at this length.
+constexpr int AD_ROWS = 128;
+constexpr int AD_ITEM = 2 + 64;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum_k(float v) {
+  v += dpp_row<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_row<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_row<0x124>(v);  // row_ror:4
+  v += dpp_row<0x128>(v);  // row_ror:8
+  return v;
+}
+
+__global__ __launch_bounds__(256) void attn_decode_split_kernel(const float* __restrict__ q, int ldq,
+                                                                const float* __restrict__ kc,
+                                                                const float* __restrict__ vc, int H, int P,
+                                                                const int* __restrict__ pos_dev,
+                                                                float* __restrict__ part, int nsmax) {
+  __shared__ float wp[4][AD_ITEM];
+  const int h = blockIdx.x, b = blockIdx.y, sp = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, grp = lane >> 4, dq = (lane & 15) * 4;
+  const int len = *pos_dev + 1;
+  if (sp * AD_ROWS >= len) return;  // no rows: the combine kernel skips this split
+  const size_t head_off = ((size_t)b * H + h) * (size_t)P * 64;
+  const int j0 = sp * AD_ROWS + wave * 32;
+  const int n = min(32, len - j0);  // this wave's rows (<= 0: none)
+  float m = -INFINITY, lsum = 0.f;
+  float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n > 0) {
+    const float4 q4 = *reinterpret_cast<const float4*>(q + (size_t)b * ldq + h * 64 + dq);
+    const float* Kh = kc + head_off + (size_t)j0 * 64 + dq;
+    const float* Vh = vc + head_off + (size_t)j0 * 64 + dq;
+    float4 k4[8], v4[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int r = min(4 * t + grp, n - 1);
+      k4[t] = *reinterpret_cast<const float4*>(Kh + (size_t)r * 64);
+      v4[t] = *reinterpret_cast<const float4*>(Vh + (size_t)r * 64);
+    }
+    float s[8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float dot = row16_sum_k(q4.x * k4[t].x + q4.y * k4[t].y + q4.z * k4[t].z + q4.w * k4[t].w);
+      s[t] = 4 * t + grp < n ? dot * 0.125f : -INFINITY;  // 1 / sqrt(64)
+      mb = fmaxf(mb, s[t]);
+    }
+    mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+    m = mb;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float p = s[t] == -INFINITY ? 0.f : expf(s[t] - m);
+      lsum += p;
+      o4.x += p * v4[t].x;
+      o4.y += p * v4[t].y;
+      o4.z += p * v4[t].z;
+      o4.w += p * v4[t].w;
+    }
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {  // sum over the 4 row groups
+      lsum += __shfl_xor(lsum, o, 64);
+      o4.x += __shfl_xor(o4.x, o, 64);
+      o4.y += __shfl_xor(o4.y, o, 64);
+      o4.z += __shfl_xor(o4.z, o, 64);
+      o4.w += __shfl_xor(o4.w, o, 64);
+    }
+  }
+  if (lane < 16) {
+    wp[wave][2 + dq] = o4.x;
+    wp[wave][3 + dq] = o4.y;
+    wp[wave][4 + dq] = o4.z;
+    wp[wave][5 + dq] = o4.w;
+  }
+  if (lane == 0) {
+    wp[wave][0] = m;
+    wp[wave][1] = lsum;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wp[w][0]);
+    float Ls = 0.f, o = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      if (wp[w][0] == -INFINITY) continue;
+      const float f = expf(wp[w][0] - M);
+      Ls += wp[w][1] * f;
+      o += wp[w][2 + tid] * f;
+    }
+    float* dst = part + (((size_t)b * H + h) * nsmax + sp) * AD_ITEM;
+    dst[2 + tid] = o;
+    if (tid == 0) {
+      dst[0] = M;
+      dst[1] = Ls;
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void attn_decode_combine_kernel(const float* __restrict__ part, int H, int nsmax,
+                                                                 const int* __restrict__ pos_dev,
+                                                                 float* __restrict__ out, int ldo) {
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int ns = (*pos_dev + 1 + AD_ROWS - 1) / AD_ROWS;
+  const float* it = part + ((size_t)b * H + h) * nsmax * AD_ITEM;
+  float M = -INFINITY;
+  for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, it[sp * AD_ITEM]);
+  float Ls = 0.f, o = 0.f;
+  for (int sp = 0; sp < ns; ++sp) {
+    const float ms = it[sp * AD_ITEM];
+    if (ms == -INFINITY) continue;
+    const float f = expf(ms - M);
+    Ls += it[sp * AD_ITEM + 1] * f;
+    o += it[sp * AD_ITEM + 2 + tid] * f;
+  }
+  out[(size_t)b * ldo + h * 64 + tid] = o / Ls;
+}
+
+size_t attn_decode_work_floats(int B, int n_head, int n_pos) {
+  return (size_t)B * n_head * ((n_pos + AD_ROWS - 1) / AD_ROWS) * AD_ITEM;
+}
+
 void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc, int n_head,
-                        int n_pos, const int* pos_dev, float* out, int ldo) {
+                        int n_pos, const int* pos_dev, float* out, int ldo, float* work) {
   // head_dim = ldq-independent: derived by the caller into n_head via ldo.
   const int hd = ldo / n_head;
+  if (hd == 64 && work) {
+    const int nsmax = (n_pos + AD_ROWS - 1) / AD_ROWS;
+    attn_decode_split_kernel<<<dim3(n_head, B, nsmax), 256, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, work,
+                                                                    nsmax);
+    attn_decode_combine_kernel<<<dim3(n_head, B), 64, 0, s>>>(work, n_head, nsmax, pos_dev, out, ldo);
+    return;
+  }
   const size_t smem = (336 + (size_t)n_pos) * sizeof(float);
   attn_decode_kernel<<<dim3(n_head, B), 256, smem, s>>>(q, ldq, kc, vc, n_head, n_pos, hd, pos_dev, out, ldo);
 }
@@ -572,7 +729,7 @@ template <int WT>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const float* __restrict__ A, int lda,
                                                           const void* __restrict__ W, const float* __restrict__ bias,
                                                           float* __restrict__ C, long ldc, int M, int N, int K,
-                                                          int epi) {
+                                                          int epi, SkinnyQkv qkv) {
   __shared__ float red[4][32][33];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, hh = lane >> 5;
@@ -617,6 +774,19 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const float* __restric
     if (m >= M || n >= N) continue;
     const float v = ((red[0][mi][ni] + red[1][mi][ni]) + red[2][mi][ni]) + red[3][mi][ni];
     const float bv = bias ? bias[n] : 0.f;
+    if (qkv.q) {
+      const int d = qkv.d;
+      if (n < d) {
+        qkv.q[(size_t)m * qkv.ldq + n] = v + bv;
+      } else {
+        const int cc = n - (n < 2 * d ? d : 2 * d);
+        const int hd = d / qkv.kv.n_head;
+        const int h = cc / hd, dd = cc - h * hd;
+        float* base = n < 2 * d ? qkv.kv.k : qkv.kv.v;
+        base[(((size_t)m * qkv.kv.n_head + h) * qkv.kv.n_pos + *qkv.pos_dev) * hd + dd] = v + bv;
+      }
+      continue;
+    }
     float* cp = C + (size_t)m * ldc + n;
     if (epi == EPI_BIAS) *cp = v + bv;
     else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
@@ -625,14 +795,116 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const float* __restric
   }
 }
 
+// The same for at most 16 rows (a decode batch) on v_mfma_f32_16x16x4f32,
+// whose 16-wide tiles waste less of the matrix unit on absent rows and give
+// twice as many workgroups: lane l supplies A[l%16][l/16] and B[l/16][l%16]
+// and holds D[(l/16)*4 + i][l%16] in accumulator i. Step e pairs the four
+// k = k0 + q*KQ + e (q = l/16, KQ = a quarter of the wave's K range), so a
+// lane again reads contiguous runs.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int WT>
+__device__ __forceinline__ void load4(const void* W, size_t idx, float* out) {
+  if (WT == W_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + idx);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(W) + idx);
+    out[0] = __uint_as_float(u.x << 16); out[1] = __uint_as_float(u.x & 0xffff0000u);
+    out[2] = __uint_as_float(u.y << 16); out[3] = __uint_as_float(u.y & 0xffff0000u);
+  }
+}
+
+template <int WT, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny16_kernel(const float* __restrict__ A, int lda,
+                                                                const void* __restrict__ W,
+                                                                const float* __restrict__ bias, float* __restrict__ C,
+                                                                long ldc, int M, int N, int K, int epi, SkinnyQkv qkv) {
+  __shared__ float red[NW][16][17];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, qq = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int KW = K / NW, KQ = KW / 4;
+  const int k0 = wave * KW + qq * KQ;  // this lane's run: [k0, k0 + KQ)
+  const float* arow = A + (size_t)min(r, M - 1) * lda + k0;
+  const size_t wrow = (size_t)min(n0 + r, N - 1) * K + k0;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  constexpr int DEPTH = 4;
+  const int nch = KQ / 4;
+  float a[DEPTH][4], w[DEPTH][4];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    const int k = min(d, nch - 1) * 4;
+    load4<W_F32>(arow, k, a[d]);
+    load4<WT>(W, wrow + k, w[d]);
+  }
+  for (int c0 = 0; c0 < nch; c0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      if (c0 + d < nch) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[d][e], w[d][e], acc, 0, 0, 0);
+      }
+      const int kn = min(c0 + d + DEPTH, nch - 1) * 4;  // refill (a repeat past the end)
+      load4<W_F32>(arow, kn, a[d]);
+      load4<WT>(W, wrow + kn, w[d]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][qq * 4 + i][r] = acc[i];
+  __syncthreads();
+  if (tid < 256) {
+    const int mi = tid >> 4, ni = tid & 15;
+    const int m = mi, n = n0 + ni;
+    if (m < M && n < N) {
+      float v = red[0][mi][ni];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) v += red[ww][mi][ni];
+      const float bv = bias ? bias[n] : 0.f;
+      if (qkv.q) {
+        const int d = qkv.d;
+        if (n < d) {
+          qkv.q[(size_t)m * qkv.ldq + n] = v + bv;
+        } else {
+          const int cc = n - (n < 2 * d ? d : 2 * d);
+          const int hd = d / qkv.kv.n_head;
+          const int h = cc / hd, dd = cc - h * hd;
+          float* base = n < 2 * d ? qkv.kv.k : qkv.kv.v;
+          base[(((size_t)m * qkv.kv.n_head + h) * qkv.kv.n_pos + *qkv.pos_dev) * hd + dd] = v + bv;
+        }
+      } else {
+        float* cp = C + (size_t)m * ldc + n;
+        if (epi == EPI_BIAS) *cp = v + bv;
+        else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
+        else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
+        else *cp = v;
+      }
+    }
+  }
+}
+
+static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias,
+                          float* C, long ldc, int M, int N, int K, int epi, const SkinnyQkv& qkv) {
+  if (M > 64 || K % 64 != 0 || lda % 4 != 0) return false;
+  if (M <= 16) {
+    // (8 waves with twice the loads in flight measured slower: each wave
+    // instruction already touches 16 rows, the address units saturate)
+    const dim3 grid((N + 15) / 16);
+    if (wtype == W_F32)
+      gemm_skinny16_kernel<W_F32, 4><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv);
+    else
+      gemm_skinny16_kernel<W_BF16, 4><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv);
+    return true;
+  }
+  dim3 grid((N + 31) / 32, (M + 31) / 32);
+  if (wtype == W_F32) gemm_skinny_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv);
+  else gemm_skinny_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv);
+  return true;
+}
+
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
                  long ldc, int M, int N, int K, int epi) {
-  if (M <= 64 && K % 64 == 0 && lda % 4 == 0) {
-    dim3 grid((N + 31) / 32, (M + 31) / 32);
-    if (wtype == W_F32) gemm_skinny_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
-    else gemm_skinny_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
-    return;
-  }
+  if (launch_skinny(s, A, lda, W, wtype, bias, C, ldc, M, N, K, epi, SkinnyQkv{})) return;
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
   if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
   else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);

@@ -118,6 +118,7 @@ struct rtg_cache {
   uint32_t* token_dev = nullptr;
   uint32_t* ids_dev = nullptr;   // [B][P] generated ids
   uint32_t* ids_in = nullptr;    // [B*P] prompt ids
+  float* att_work = nullptr;     // per-split partials of decode attention
   // work buffers, capacity in rows
   size_t rows_cap = 0;
   float *x = nullptr, *ln = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
@@ -187,6 +188,7 @@ static rtg_cache* cache_create(const rtg_model* m, size_t batch) {
     HIPX(hipMalloc(&c->token_dev, std::max<size_t>(batch, 1) * 4));
     HIPX(hipMalloc(&c->ids_dev, std::max<size_t>(batch * P, 1) * 4));
     HIPX(hipMalloc(&c->ids_in, std::max<size_t>(batch * P, 1) * 4));
+    HIPX(hipMalloc(&c->att_work, std::max<size_t>(attn_decode_work_floats((int)batch, (int)H, (int)P), 1) * 4));
     for (auto& e : c->ev) HIPX(hipEventCreate(&e));
     HIPX(hipMemsetAsync(c->pos_dev, 0, 256, c->stream));
     HIPX(hipMemsetAsync(c->step_dev, 0, 256, c->stream));
@@ -269,7 +271,7 @@ static void enqueue_decode_step(rtg_cache* c) {
       KvDst kv = kv_layer(c, l);
       launch_layernorm(s, c->x, L.ln1w, L.ln1b, eps, B, d, c->ln);
       launch_gemv_qkv(s, B, L.wqkv, m->wtype, L.bqkv, c->ln, d, c->qkv, d, d, kv, c->pos_dev);
-      launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d);
+      launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d, c->att_work);
       launch_gemv(s, B, L.waproj, m->wtype, L.baproj, c->att, d, c->x, d, d, d, EPI_BIAS_RESID);
       launch_layernorm(s, c->x, L.ln2w, L.ln2b, eps, B, d, c->ln);
       launch_gemv(s, B, L.wfc, m->wtype, L.bfc, c->ln, d, c->h, 4 * d, 4 * d, d, EPI_BIAS_GELU);
@@ -387,8 +389,15 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   set_counters(c, (int)n - 1, 0);
   launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev);
   HIPX(hipEventRecord(c->ev[1], s));
-  ensure_graph(c);
-  for (size_t i = 1; i < steps; ++i) HIPX(hipGraphLaunch(c->graph_exec, s));
+  // RTG_NO_GRAPH=1: enqueue each step's kernels directly instead of replaying
+  // the captured step graph (for per-kernel profiling; same results).
+  const char* ng = getenv("RTG_NO_GRAPH");
+  if (ng && ng[0] == '1') {
+    for (size_t i = 1; i < steps; ++i) enqueue_decode_step(c);
+  } else {
+    ensure_graph(c);
+    for (size_t i = 1; i < steps; ++i) HIPX(hipGraphLaunch(c->graph_exec, s));
+  }
   HIPX(hipEventRecord(c->ev[2], s));
   // Optional profiling pass: rewind to the first decode step and replay the
   // steps launch by launch with events around the persistent kernel. Inputs
@@ -848,7 +857,7 @@ void rtg_cache_destroy(rtg_cache* c) {
   if (c->pstate) persistent_state_destroy(c->pstate);
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
-                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->logits})
+                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits})
     if (p) hipFree(p);
   for (auto e : c->ev)
     if (e) hipEventDestroy(e);
