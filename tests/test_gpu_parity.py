@@ -246,6 +246,68 @@ def test_batched_forward_logits(O):
         assert_logits_close(lg2[b], om.forward_cached(nxt[b], oc), f"batched step seq {b}")
 
 
+def _decode_parity(O, sd, sh, m, n_prompt, n_new, n_logit_steps, stream):
+    """Greedy ids over n_new steps and the logits of the prefill plus
+    n_logit_steps single-token steps, against the oracle."""
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    prompt = synth.make_tokens(n_prompt, sh.vocab_size, stream=stream)
+    ref_ids = om.generate_cached(prompt, n_new)
+    assert m.generate_cached(prompt, n_new, 0.0) == ref_ids
+    c, oc = m.new_cache(), om.new_cache()
+    assert_logits_close(m.forward_cached(prompt, c), om.forward_cached(prompt, oc), "prefill")
+    for t in range(n_prompt, n_prompt + n_logit_steps):
+        tok = [ref_ids[t]]
+        assert_logits_close(m.forward_cached(tok, c), om.forward_cached(tok, oc), f"step {t}")
+
+
+def test_medium_decode(O):
+    """GPT-2 medium (configuration c3's model): persistent decode instance for d=1024."""
+    sh = synth.SHAPES["medium"]
+    sd = synth.make_weights(sh)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    print("[gpu] medium parity", flush=True)
+    _decode_parity(O, sd, sh, m, 16, 24, 4, stream=400)
+    m.close()
+
+
+def test_large_decode(O):
+    """GPT-2 large, f32 (d=1280 persistent decode instance)."""
+    sh = synth.SHAPES["large"]
+    sd = synth.make_weights(sh)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    print("[gpu] large parity", flush=True)
+    _decode_parity(O, sd, sh, m, 8, 12, 2, stream=410)
+    m.close()
+
+
+def test_xl_bf16_decode(O):
+    """GPT-2 XL with bf16-rounded weights (configuration c5's storage): the
+    batch-1 persistent instance and the batched path, against the oracle fed
+    the same bf16-rounded weights."""
+    sh = synth.SHAPES["xl"]
+    sd = synth.make_weights(sh, bf16=True)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh), storage="bf16")
+    print("[gpu] xl bf16 parity", flush=True)
+    _decode_parity(O, sd, sh, m, 8, 10, 2, stream=420)
+    prompts = np.stack([synth.make_tokens(8, sh.vocab_size, stream=430 + b) for b in range(2)])
+    out = m.generate_cached_batched(prompts, 6)
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    for b in range(2):
+        assert out[b].tolist() == om.generate_cached(prompts[b], 6)
+    m.close()
+
+
+def test_bf16_batched_decode_matches_single():
+    """bf16 weights through the batched decode path (B=3) against single runs."""
+    sh = synth.SHAPES["mini"]
+    sd = synth.make_weights(sh, bf16=True)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh), storage="bf16")
+    prompts = np.stack([synth.make_tokens(10, sh.vocab_size, stream=440 + b) for b in range(3)])
+    out = m.generate_cached_batched(prompts, 20)
+    for b in range(3):
+        assert out[b].tolist() == m.generate_cached(prompts[b], 20, 0.0)
+
+
 def test_bf16_storage_matches_oracle(O):
     sh = synth.SHAPES["mini"]
     sd = synth.make_weights(sh, bf16=True)
