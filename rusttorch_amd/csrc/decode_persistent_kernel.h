@@ -44,7 +44,7 @@ constexpr int NGLUE = 1 + NA;       // leader + helpers
 constexpr int NTHREADS = (1 + NA + NC) * 64;
 constexpr int HD = 64;              // head_dim of every GPT-2 size
 constexpr int CMAX = 16;            // attention chunks per head
-constexpr int ITEM_WORDS = 2 + HD;  // m, l, o[64]
+constexpr int ITEM_WORDS = HD + 2;  // o[64], m, l
 constexpr int MAX_ITEMS = 64;       // heads * chunks merged by the consumers
 constexpr int MAXW = 8;             // polled words per glue lane per round (16 spills registers)
 constexpr int PART_MAX = 1536;      // segment partials per workgroup
@@ -804,11 +804,17 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
           Ls += sm.att_part[w][1] * f;
           o += sm.att_part[w][2 + lane] * f;
         }
+        // item slot: o[64], then m and l; a head in a single chunk publishes
+        // its finished output o / l and the consumers use it as it is
         u64* dst = T + p.o_att + (long)item * ITEM_SLOT;
-        tstore(dst + 2 + lane, o, tag);
-        if (lane == 0) {
-          tstore(dst, M, tag);
-          tstore(dst + 1, Ls, tag);
+        if (NCH == 1) {
+          tstore(dst + lane, o / Ls, tag);
+        } else {
+          tstore(dst + lane, o, tag);
+          if (lane == 0) {
+            tstore(dst + HD, M, tag);
+            tstore(dst + HD + 1, Ls, tag);
+          }
         }
       }
     }
@@ -817,22 +823,28 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
       bias = lane < rows_here ? PK_G(float, LP.baproj)[row0 + lane] : 0.f;
     }
-    glue_fetch<ITEM_WORDS, ITEM_SLOT>(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
-    if (leader) PK_TRACE(p, tb + 14, lane);
-    glue_barrier(sm, gen, lane, p.err);
-    // merge the chunks of each head; heads are spread over the glue waves
-    for (int h = gw; h < H; h += NGLUE) {
-      float M = -INFINITY;
-      for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS]);
-      float Ls = 0.f, o = 0.f;
-      for (int c = 0; c < NCH; ++c) {
-        const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
-        if (it[0] == -INFINITY) continue;
-        const float f = expf(it[0] - M);
-        Ls += it[1] * f;
-        o += it[2 + lane] * f;
+    if (NCH == 1) {
+      // one item per head: the heads' outputs are the projection input
+      glue_fetch<HD, ITEM_SLOT>(T + p.o_att, H * HD, tag, sm.in_vec[0], gl, p.err);
+      if (leader) PK_TRACE(p, tb + 14, lane);
+    } else {
+      glue_fetch<ITEM_WORDS, ITEM_SLOT>(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
+      if (leader) PK_TRACE(p, tb + 14, lane);
+      glue_barrier(sm, gen, lane, p.err);
+      // merge the chunks of each head; heads are spread over the glue waves
+      for (int h = gw; h < H; h += NGLUE) {
+        float M = -INFINITY;
+        for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS + HD]);
+        float Ls = 0.f, o = 0.f;
+        for (int c = 0; c < NCH; ++c) {
+          const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
+          if (it[HD] == -INFINITY) continue;
+          const float f = expf(it[HD] - M);
+          Ls += it[HD + 1] * f;
+          o += it[lane] * f;
+        }
+        sm.in_vec[0][h * HD + lane] = o / Ls;
       }
-      sm.in_vec[0][h * HD + lane] = o / Ls;
     }
     glue_barrier(sm, gen, lane, p.err);
     if (leader) {

@@ -260,6 +260,14 @@ def _decode_parity(O, sd, sh, m, n_prompt, n_new, n_logit_steps, stream):
         assert_logits_close(m.forward_cached(tok, c), om.forward_cached(tok, oc), f"step {t}")
 
 
+def test_small_long_context_decode(O):
+    """Batch-1 decode past 128 positions: the persistent step splits each
+    head's positions into chunks and merges their partial softmaxes."""
+    sd, sh, m = gpu_model("small")
+    print("[gpu] small long-context parity", flush=True)
+    _decode_parity(O, sd, sh, m, 200, 12, 3, stream=450)
+
+
 def test_medium_decode(O):
     """GPT-2 medium (configuration c3's model): persistent decode instance for d=1024."""
     sh = synth.SHAPES["medium"]
