@@ -229,6 +229,27 @@ __device__ __forceinline__ float wsum_dpp(float v) {
   return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
          (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
 }
+// Combine each lane's value with the lane 16 (or 32) apart through gfx950's
+// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip): the two
+// swapped registers hold the lane's own value and its partner's, so their sum
+// (max) is the pairwise sum (max), identical in both lanes.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float wmax(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -582,8 +603,7 @@ __device__ __forceinline__ void att_window_t(const float* ldsK, const float* lds
     s[t] = 4 * t + grp < n ? dot * scale : -INFINITY;
     mb = fmaxf(mb, s[t]);
   }
-  mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-  mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+  mb = xor32_max(xor16_max(mb));
   const float mn = fmaxf(m, mb);
   const float corr = m == -INFINITY ? 0.f : expf(m - mn);
   lsum *= corr;
@@ -767,14 +787,11 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
           m = mn;
         }
         // sum over the 4 row groups
-#pragma unroll
-        for (int o = 16; o < 64; o <<= 1) {
-          lsum += __shfl_xor(lsum, o, 64);
-          o4.x += __shfl_xor(o4.x, o, 64);
-          o4.y += __shfl_xor(o4.y, o, 64);
-          o4.z += __shfl_xor(o4.z, o, 64);
-          o4.w += __shfl_xor(o4.w, o, 64);
-        }
+        lsum = xor32_sum(xor16_sum(lsum));
+        o4.x = xor32_sum(xor16_sum(o4.x));
+        o4.y = xor32_sum(xor16_sum(o4.y));
+        o4.z = xor32_sum(xor16_sum(o4.z));
+        o4.w = xor32_sum(xor16_sum(o4.w));
         if (lane < 16) {
           sm.att_part[hw][2 + dq + 0] = o4.x;
           sm.att_part[hw][2 + dq + 1] = o4.y;

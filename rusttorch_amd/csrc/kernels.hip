@@ -350,6 +350,26 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_row(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+// Pairwise combination with the lane 16 / 32 apart via gfx950's permlane
+// swaps (VALU): the two swapped registers are the lane's value and its
+// partner's, so their sum / max is the same in both lanes.
+__device__ __forceinline__ float xor16_sum_k(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum_k(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max_k(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max_k(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float row16_sum_k(float v) {
   v += dpp_row<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_row<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -392,8 +412,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(const float* __r
       s[t] = 4 * t + grp < n ? dot * 0.125f : -INFINITY;  // 1 / sqrt(64)
       mb = fmaxf(mb, s[t]);
     }
-    mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+    mb = xor32_max_k(xor16_max_k(mb));
     m = mb;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
@@ -404,14 +423,12 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(const float* __r
       o4.z += p * v4[t].z;
       o4.w += p * v4[t].w;
     }
-#pragma unroll
-    for (int o = 16; o < 64; o <<= 1) {  // sum over the 4 row groups
-      lsum += __shfl_xor(lsum, o, 64);
-      o4.x += __shfl_xor(o4.x, o, 64);
-      o4.y += __shfl_xor(o4.y, o, 64);
-      o4.z += __shfl_xor(o4.z, o, 64);
-      o4.w += __shfl_xor(o4.w, o, 64);
-    }
+    // sum over the 4 row groups
+    lsum = xor32_sum_k(xor16_sum_k(lsum));
+    o4.x = xor32_sum_k(xor16_sum_k(o4.x));
+    o4.y = xor32_sum_k(xor16_sum_k(o4.y));
+    o4.z = xor32_sum_k(xor16_sum_k(o4.z));
+    o4.w = xor32_sum_k(xor16_sum_k(o4.w));
   }
   if (lane < 16) {
     wp[wave][2 + dq] = o4.x;
@@ -1121,7 +1138,7 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
       s[i] = j <= qpos ? s[i] * 0.125f : -INFINITY;
       bm = fmaxf(bm, s[i]);
     }
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    bm = xor32_max_k(bm);
     const float mn = fmaxf(m, bm);
     const float corr = m == -INFINITY ? 0.f : expf(m - mn);
     float ps = 0.f;
@@ -1152,7 +1169,7 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
       o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.w, s[4 * g + 3], o1, 0, 0, 0);
     }
   }
-  l += __shfl_xor(l, 32, 64);
+  l = xor32_sum_k(l);
   if (qvalid) {
     const float inv = 1.0f / l;
     float* orow = out + ((size_t)sidx * T + qi) * d + h * 64;

@@ -265,7 +265,11 @@ def test_small_long_context_decode(O):
     head's positions into chunks and merges their partial softmaxes."""
     sd, sh, m = gpu_model("small")
     print("[gpu] small long-context parity", flush=True)
+    # 200: two chunks per head, each staged whole in LDS and shared by all waves
     _decode_parity(O, sd, sh, m, 200, 12, 3, stream=450)
+    # 650: the chunk count is capped (12 heads x 5 chunks), chunks exceed the
+    # LDS stage and are streamed through it window by window
+    _decode_parity(O, sd, sh, m, 650, 4, 2, stream=451)
 
 
 def test_medium_decode(O):
