@@ -26,6 +26,37 @@ const void* kernel_1600_50257_bf16();
 }  // namespace pk
 
 namespace {
+// LayerNorm folded into the GEMV that follows it: for output row r of
+// W^T[N][K] (row r contiguous), s[r] = sum_k W[r][k] g[k] and
+// c[r] = bias[r] + sum_k W[r][k] b[k], accumulated in double. One wave per row.
+__global__ void ln_fold_kernel(const void* W, int wtype, int N, int K, const float* g, const float* b,
+                               const float* bias, float* s, float* c) {
+  const int r = blockIdx.x * (blockDim.x / 64) + (int)(threadIdx.x / 64);
+  const int lane = threadIdx.x & 63;
+  if (r >= N) return;
+  double ss = 0.0, cc = 0.0;
+  for (int k = lane; k < K; k += 64) {
+    const float w = wtype == W_F32 ? static_cast<const float*>(W)[(long)r * K + k]
+                                   : __uint_as_float((uint32_t)static_cast<const uint16_t*>(W)[(long)r * K + k] << 16);
+    ss += (double)w * (double)g[k];
+    cc += (double)w * (double)b[k];
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    ss += __shfl_xor(ss, o, 64);
+    cc += __shfl_xor(cc, o, 64);
+  }
+  if (lane == 0) {
+    s[r] = (float)ss;
+    c[r] = (float)((bias ? (double)bias[r] : 0.0) + cc);
+  }
+}
+
+bool ln_fold(const void* W, int wtype, int N, int K, const float* g, const float* b, const float* bias, float* s,
+             float* c) {
+  hipLaunchKernelGGL(ln_fold_kernel, dim3((N + 3) / 4), dim3(256), 0, 0, W, wtype, N, K, g, b, bias, s, c);
+  return hipGetLastError() == hipSuccess;
+}
+
 struct Inst {
   int d, v, wtype;
   const void* (*fn)();
@@ -44,6 +75,7 @@ struct PersistentPlan {
   pk::Params base{};
   pk::LayerPtrs* layers_dev = nullptr;
   void* zeros = nullptr;
+  float* fold = nullptr;  // folded LayerNorm constants (LayerPtrs::sq etc., Params::sl/cl)
 };
 
 struct PersistentState {
@@ -70,11 +102,25 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   for (const Inst& in : kInstances)
     if (in.d == d && in.v == V && in.wtype == w.wtype) fn = in.fn();
   if (!fn) return pl;
+  // folded constants: per layer sq, cq [3d] and sf, cf [4d]; then sl, cl [V]
+  const size_t per_layer = 2 * (size_t)(3 * d) + 2 * (size_t)(4 * d);
+  const size_t fold_floats = per_layer * L + 2 * (size_t)V;
+  if (hipDeviceSynchronize() != hipSuccess || hipMalloc(&pl->fold, fold_floats * 4) != hipSuccess) return pl;
   std::vector<pk::LayerPtrs> lp(L);
   for (int i = 0; i < L; ++i) {
     const PersistentLayer& s = w.layers[i];
-    lp[i] = {s.wqkv, s.waproj, s.wfc, s.wmproj, s.bqkv, s.baproj, s.bfc, s.bmproj, s.ln1w, s.ln1b, s.ln2w, s.ln2b};
+    float* f = pl->fold + per_layer * i;
+    float *sq = f, *cq = f + 3 * d, *sf = f + 6 * d, *cf = f + 10 * d;
+    if (!ln_fold(s.wqkv, w.wtype, 3 * d, d, s.ln1w, s.ln1b, s.bqkv, sq, cq) ||
+        !ln_fold(s.wfc, w.wtype, 4 * d, d, s.ln2w, s.ln2b, s.bfc, sf, cf))
+      return pl;
+    lp[i] = {s.wqkv, s.waproj, s.wfc, s.wmproj, s.bqkv, s.baproj, s.bfc, s.bmproj, s.ln1w, s.ln1b, s.ln2w, s.ln2b,
+             sq, cq, sf, cf};
   }
+  float* sl = pl->fold + per_layer * L;
+  float* cl = sl + V;
+  if (!ln_fold(w.wte, w.wtype, V, d, w.lnfw, w.lnfb, nullptr, sl, cl) || hipDeviceSynchronize() != hipSuccess)
+    return pl;
   if (hipMalloc(&pl->layers_dev, sizeof(pk::LayerPtrs) * L) != hipSuccess) return pl;
   if (hipMemcpy(pl->layers_dev, lp.data(), sizeof(pk::LayerPtrs) * L, hipMemcpyHostToDevice) != hipSuccess)
     return pl;
@@ -86,6 +132,8 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   p.wpe = w.wpe;
   p.lnfw = w.lnfw;
   p.lnfb = w.lnfb;
+  p.sl = sl;
+  p.cl = cl;
   p.L = L;
   p.P = P;
   p.eps = w.cfg.layer_norm_epsilon;
@@ -107,6 +155,7 @@ void persistent_plan_destroy(PersistentPlan* pl) {
   if (!pl) return;
   if (pl->layers_dev) hipFree(pl->layers_dev);
   if (pl->zeros) hipFree(pl->zeros);
+  if (pl->fold) hipFree(pl->fold);
   delete pl;
 }
 

@@ -46,8 +46,12 @@ constexpr int HD = 64;              // head_dim of every GPT-2 size
 constexpr int CMAX = 16;            // attention chunks per head
 constexpr int ITEM_WORDS = HD + 2;  // o[64], m, l
 constexpr int MAX_ITEMS = 64;       // heads * chunks merged by the consumers
-constexpr int MAXW = 8;             // polled words per glue lane per round (16 spills registers)
 constexpr int PART_MAX = 1536;      // segment partials per workgroup
+// GEMV phase types, each with its own input-ready counter. A glue wave counts
+// itself once per layer in each; every workgroup owns rows of the FC phase in
+// every supported shape, so no wave can run a whole layer ahead of another and
+// a count of NGLUE * (l + 1) means that every glue wave delivered layer l.
+enum { PH_QKV = 0, PH_PROJ = 1, PH_FC = 2, PH_MLP = 3, PH_LM = 4 };
 constexpr int KVS = 128;            // cached positions of one item staged in LDS
 // Exchange layout: each producer owns a slot of whole 128-byte lines, so no
 // two producers ever write the same line and readers of one producer's words
@@ -67,12 +71,17 @@ typedef unsigned long long u64;
 struct LayerPtrs {
   const void *wqkv, *waproj, *wfc, *wmproj;
   const float *bqkv, *baproj, *bfc, *bmproj, *ln1w, *ln1b, *ln2w, *ln2b;
+  // LayerNorm folded into the following GEMV (computed once at load time):
+  // for output row r, s[r] = sum_k W[r][k] g[k] and c[r] = bias[r] +
+  // sum_k W[r][k] b[k], so LN(x) @ W + bias = inv_std * (W.(x*g) - mean * s) + c.
+  const float *sq, *cq, *sf, *cf;
 };
 
 struct Params {
   const LayerPtrs* layers;
   const void* wte;
   const float *wpe, *lnfw, *lnfb;
+  const float *sl, *cl;  // ln_f folded into the tied LM head, as for the layers
   int L, P;
   float eps;
   float* kc;  // [L][H][P][HD]
@@ -150,10 +159,15 @@ struct Smem {
   float x2raw[D];          // residual after attention
   float part[PART_MAX];
   float stage[MAX_ITEMS * ITEM_WORDS];
-  float att_q[HD], att_k[HD], att_v[HD];
   float kv_k[KVS * HD], kv_v[KVS * HD];  // K/V rows [j0, j0 + KVS) of this workgroup's item
   float att_part[NA][ITEM_WORDS];
-  unsigned gemv_ready, gemv_done, glue_cnt;
+  float att_q[HD], att_k[HD], att_v[HD];
+  // in_ready[phase]: +1 per glue wave once its share of that phase's GEMV
+  // input is in LDS (one counter per phase type, see PH_QKV..PH_LM);
+  // gemv_done: +1 per GEMV wave per phase; glue_cnt: glue-wave barrier;
+  // att_go: layers whose q/k/v the leader has put in LDS; att_cnt: helpers
+  // that finished the layer's attention.
+  unsigned in_ready[5], gemv_done, glue_cnt, att_go, att_cnt;
   u64 trace_t0;
   unsigned trace_rel[TRACE_N];
 };
@@ -298,11 +312,18 @@ struct V16<W_BF16> {
 #ifndef PK_PACE
 #define PK_PACE 12
 #endif
-// PACE > 0: sleep PACE*64 clocks between loads while the wave's next input
-// is not ready yet (*ready < next), so a refill does not flood this CU's
-// memory queue ahead of the exchanges; the sleep is the only conditional
-// part, the loads stay in fixed order.
-template <int WT, int MAXSEG, class GEO, int PACE = PK_PACE>
+// PACE > 0: sleep up to PACE*64 clocks between loads while the wave's next
+// input is not ready yet (*ready < next), so a refill does not flood this
+// CU's memory queue ahead of the exchanges; the sleep is cut short (to 128
+// clocks) once the input is ready, and is the only conditional part: the
+// loads stay in fixed order.
+#ifndef PK_LM_NT
+#define PK_LM_NT 1
+#endif
+#ifndef PK_W_NT
+#define PK_W_NT 1
+#endif
+template <int WT, int MAXSEG, class GEO, int PACE = PK_PACE, bool NT = PK_W_NT>
 __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], const void* W, const void* dummy, int wg,
                                           int cw, int lane, int seg_base, unsigned* ready = nullptr,
                                           unsigned next = 0) {
@@ -324,8 +345,10 @@ __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], co
       const int li = (GEO::VR % 64 == 0) ? lane : min(lane, max(0, min(GEO::VR - j * 64, 64) - 1));
       // non-temporal: weights are streamed once per step (measured ~15% more
       // streaming bandwidth than plain loads on this part)
-      buf[i] = __builtin_nontemporal_load(PK_G(Vec, rowp) + li);
-      if (PACE > 0 && i + 1 < GEO::SPW && lds_load(ready) < next) __builtin_amdgcn_s_sleep(PACE);
+      if constexpr (NT) buf[i] = __builtin_nontemporal_load(PK_G(Vec, rowp) + li);
+      else buf[i] = PK_G(Vec, rowp)[li];
+      if (PACE > 0 && i + 1 < GEO::SPW)
+        for (int t = 0; t < PACE / 2 && lds_load(ready) < next; ++t) __builtin_amdgcn_s_sleep(2);
     }
     if (++j == GEO::SPR) {
       j = 0;
@@ -397,9 +420,10 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
   const __attribute__((address_space(4))) LayerPtrs* LP = PK_C(LayerPtrs, p.layers);
   // The code below issues every buffer refill unconditionally (the last
   // layer is peeled) so each consume waits only for its own buffer.
-  auto compute_and_signal = [&](auto& buf, const float* x, auto geo_tag) {
+  auto compute_and_signal = [&](auto& buf, const float* x, auto geo_tag, int ph, int l) {
     typedef decltype(geo_tag) GEO;
-    lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
+    lds_wait_ge(&sm.in_ready[ph], (unsigned)(l + 1) * NGLUE, p.err);
+    ++seq;
     if (cw == 0) PK_TRACE(p, 1024 + 2 * (int)seq, lane);
     seg_compute<WT, MS, GEO>(buf, x, sm.part, wg, cw, lane, 0);
     if (cw == 0) PK_TRACE(p, 1025 + 2 * (int)seq, lane);
@@ -407,40 +431,45 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     if (lane == 0) lds_add(&sm.gemv_done, 1);
   };
   seg_issue<WT, MS, GQ, 0>(A, LP[0].wqkv, dz, wg, cw, lane, 0);  // needed first: no pacing
-  seg_issue<WT, MS, GP>(B, LP[0].waproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
+  // each refill is paced until the input of this wave's next compute is ready
+  auto rdy = [&](int ph) { return &sm.in_ready[ph]; };
+  seg_issue<WT, MS, GP>(B, LP[0].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), NGLUE);
   for (int l = 0; l + 1 < p.L; ++l) {
-    compute_and_signal(A, sm.in_vec[1], GQ());   // QKV; refill A with FC
-    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
-    compute_and_signal(B, sm.in_vec[0], GP());   // attention projection; refill B with MLP projection
-    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
-    compute_and_signal(A, sm.in_vec[1], GF());   // FC; refill A with next QKV
-    seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
-    compute_and_signal(B, sm.in_vec[0], GM());   // MLP projection; refill B with next attention projection
-    seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
+    const unsigned n1 = (unsigned)(l + 1) * NGLUE;
+    compute_and_signal(A, sm.in_vec[1], GQ(), PH_QKV, l);   // QKV; refill A with FC
+    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
+    compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);  // attention projection; refill B with MLP projection
+    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
+    compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);    // FC; refill A with next QKV
+    seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
+    compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);   // MLP projection; refill B with next attention projection
+    seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), n1 + NGLUE);
   }
   {  // last layer: the refills after FC / MLP projection are the LM head's chunks 0 and 1
     const int l = p.L - 1;
-    compute_and_signal(A, sm.in_vec[1], GQ());
-    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
-    compute_and_signal(B, sm.in_vec[0], GP());
-    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
-    compute_and_signal(A, sm.in_vec[1], GF());
-    seg_issue<WT, MS, GL>(A, p.wte, dz, wg, cw, lane, 0, &sm.gemv_ready, seq + 1);
-    compute_and_signal(B, sm.in_vec[0], GM());
-    seg_issue<WT, MS, GL>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, &sm.gemv_ready, seq + 1);
+    const unsigned n1 = (unsigned)(l + 1) * NGLUE;
+    compute_and_signal(A, sm.in_vec[1], GQ(), PH_QKV, l);
+    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
+    compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);
+    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
+    compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);
+    seg_issue<WT, MS, GL, PK_PACE, PK_LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
+    compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);
+    seg_issue<WT, MS, GL, PK_PACE, PK_LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE);
   }
   // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
   // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
-  lds_wait_ge(&sm.gemv_ready, ++seq, p.err);
+  lds_wait_ge(&sm.in_ready[PH_LM], NGLUE, p.err);
+  ++seq;
   constexpr int PER_CHUNK = NC * GL::SPW;
   const int rows_here = min(GL::RPW, GL::N - wg * GL::RPW);
   const int segs_here = rows_here > 0 ? rows_here * GL::SPR : 0;
   for (int base = 0; base < segs_here; base += 2 * PER_CHUNK) {
     // nothing else is in flight now: stream at full rate
     seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base);
-    seg_issue<WT, MS, GL, 0>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
+    seg_issue<WT, MS, GL, 0, PK_LM_NT>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
     seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK);
-    seg_issue<WT, MS, GL, 0>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
+    seg_issue<WT, MS, GL, 0, PK_LM_NT>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
   }
   lds_release();
   if (lane == 0) lds_add(&sm.gemv_done, 1);
@@ -470,14 +499,28 @@ __device__ __forceinline__ int slot_of(int i) {
 // and stale words are re-read until their tags equal the step's epoch. The
 // data is polled directly: with one line per producer slot, a poll costs
 // the same line requests as polling a per-producer flag would, and saves
-// the flag's extra round trip.
-template <int RPW, int SW>
-__device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, float* dst, int gl, unsigned* err) {
+// the flag's extra round trip. The NW = ceil(NMAX / 192) words of a lane in
+// a chunk of NMAX words are in flight together, so an exchange of n <= NMAX
+// words costs one polling round trip; longer ones take n / NMAX. With SCALE,
+// dst2[i] = word * g[i] as well (the LayerNorm gain applied to a GEMV input
+// whose LayerNorm is folded).
+template <int RPW, int SW, int NMAX, bool SCALE = false>
+__device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, float* dst, int gl, unsigned* err,
+                                           float* dst2 = nullptr, const float* g = nullptr) {
   constexpr int NG = NGLUE * 64;
-  for (int base = 0; base < n; base += MAXW * NG) {
-    u64 w[MAXW];
+  constexpr int NW = (NMAX + NG - 1) / NG;
+  for (int base = 0; base < n; base += NW * NG) {
+    float gv[NW];
+    if constexpr (SCALE) {
 #pragma unroll
-    for (int k = 0; k < MAXW; ++k) {
+      for (int k = 0; k < NW; ++k) {
+        const int i = base + gl + k * NG;
+        gv[k] = i < n ? PK_G(float, g)[i] : 0.f;
+      }
+    }
+    u64 w[NW];
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
       const int i = base + gl + k * NG;
       w[k] = i < n ? tload(src + slot_of<RPW, SW>(i)) : ((u64)tag << 32);
     }
@@ -485,7 +528,7 @@ __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, 
     for (;;) {
       bool all = true;
 #pragma unroll
-      for (int k = 0; k < MAXW; ++k)
+      for (int k = 0; k < NW; ++k)
         if ((unsigned)(w[k] >> 32) != tag) all = false;
       if (all) break;
       if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(err))) {
@@ -494,39 +537,46 @@ __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, 
       }
       __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-      for (int k = 0; k < MAXW; ++k) {
+      for (int k = 0; k < NW; ++k) {
         const int i = base + gl + k * NG;
         if (i < n && (unsigned)(w[k] >> 32) != tag) w[k] = tload(src + slot_of<RPW, SW>(i));
       }
     }
 #pragma unroll
-    for (int k = 0; k < MAXW; ++k) {
+    for (int k = 0; k < NW; ++k) {
       const int i = base + gl + k * NG;
-      if (i < n) dst[i] = __uint_as_float((unsigned)w[k]);
+      if (i < n) {
+        const float v = __uint_as_float((unsigned)w[k]);
+        dst[i] = v;
+        if constexpr (SCALE) dst2[i] = v * gv[k];
+      }
     }
   }
 }
 
-// LayerNorm gain/bias of this lane's columns, loaded ahead of the input poll.
+// A glue wave's share of the input of a GEMV phase of type ph is in LDS.
 template <int D>
-struct LnParams {
-  static constexpr int NK = D / 64;
-  float w[NK], b[NK];
-};
-template <int D>
-__device__ __forceinline__ void ln_prefetch(LnParams<D>& q, const float* w, const float* b, int lane) {
-#pragma unroll
-  for (int k = 0; k < LnParams<D>::NK; ++k) {
-    q.w[k] = PK_G(float, w)[lane + 64 * k];
-    q.b[k] = PK_G(float, b)[lane + 64 * k];
-  }
+__device__ __forceinline__ void glue_input_done(Smem<D>& sm, int ph, int lane) {
+  lds_release();
+  if (lane == 0) lds_add(&sm.in_ready[ph], 1);
 }
 
-// Leader only: LayerNorm of src[D] into dst (gpt2.rs:636-666, two-pass).
+// Sum over the wave, returned to every lane: DPP within each 16-lane row,
+// then the permlane swaps across rows.
+__device__ __forceinline__ float wave_sum_all(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  return xor32_sum(xor16_sum(v));
+}
+
+// Leader only: LayerNorm statistics of src[D] (gpt2.rs:636-666, two-pass:
+// mean = sum/n, var = sum((x - mean)^2)/n, inv_std = 1/sqrt(var + eps)). The
+// normalisation itself is folded into the following GEMV.
 template <int D>
-__device__ __forceinline__ void leader_layernorm(const float* src, const LnParams<D>& q, float eps, float* dst,
-                                                 int lane) {
-  constexpr int NK = LnParams<D>::NK;
+__device__ __forceinline__ void leader_ln_stats(const float* src, float eps, float& mean, float& inv_std, int lane) {
+  constexpr int NK = D / 64;
   float x[NK];
   float s = 0.f;
 #pragma unroll
@@ -534,17 +584,15 @@ __device__ __forceinline__ void leader_layernorm(const float* src, const LnParam
     x[k] = src[lane + 64 * k];
     s += x[k];
   }
-  const float mean = wsum_dpp(s) / (float)D;
+  mean = wave_sum_all(s) / (float)D;
   float v = 0.f;
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const float t = x[k] - mean;
     v += t * t;
   }
-  const float var = wsum_dpp(v) / (float)D;
-  const float inv_std = 1.0f / sqrtf(var + eps);
-#pragma unroll
-  for (int k = 0; k < NK; ++k) dst[lane + 64 * k] = (x[k] - mean) * inv_std * q.w[k] + q.b[k];
+  const float var = wave_sum_all(v) / (float)D;
+  inv_std = 1.0f / sqrtf(var + eps);
 }
 
 // ---------------------------------------------------------------------------
@@ -634,15 +682,6 @@ __device__ __forceinline__ void att_window(const float* ldsK, const float* ldsV,
   }
 }
 
-// Leader only: publish in_vec to the GEMV waves and wait for their partials.
-template <int D>
-__device__ __forceinline__ void leader_run_gemv(Smem<D>& sm, unsigned& seq, int lane, unsigned* err) {
-  lds_release();
-  ++seq;
-  if (lane == 0) __hip_atomic_store(&sm.gemv_ready, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  lds_wait_ge(&sm.gemv_done, seq * NC, err);
-}
-
 // Row sums acc(lr) = sum_j part[lr*SPR + j] (ascending j).
 template <class GEO, int D>
 __device__ __forceinline__ float row_acc(const Smem<D>& sm, int lr) {
@@ -652,6 +691,42 @@ __device__ __forceinline__ float row_acc(const Smem<D>& sm, int lr) {
   return a;
 }
 
+// Poll NW tagged words src[idx[k]] (k < n) until their tags equal the step's
+// epoch; out[k] = the words' values (0 for k >= n).
+template <int NW>
+__device__ __forceinline__ void poll_words(const u64* src, const int (&idx)[NW], int n, unsigned tag, float (&out)[NW],
+                                           unsigned* err) {
+  u64 w[NW];
+#pragma unroll
+  for (int k = 0; k < NW; ++k) w[k] = k < n ? tload(src + idx[k]) : ((u64)tag << 32);
+  unsigned spins = 0;
+  for (;;) {
+    bool all = true;
+#pragma unroll
+    for (int k = 0; k < NW; ++k)
+      if ((unsigned)(w[k] >> 32) != tag) all = false;
+    if (all) break;
+    if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(err))) {
+      raise_err(err, 1u);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int k = 0; k < NW; ++k)
+      if (k < n && (unsigned)(w[k] >> 32) != tag) w[k] = tload(src + idx[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < NW; ++k) out[k] = __uint_as_float((unsigned)w[k]);
+}
+
+// The glue waves (leader + helpers). Per GEMV phase each glue wave fetches a
+// third of the phase's input into LDS and counts itself in in_ready; the GEMV
+// waves start from that count, and the leader (which also needs the whole
+// input: LayerNorm statistics, residuals) waits for the same count, then for
+// the GEMV waves, and runs the epilogue. LayerNorm is folded into the GEMV
+// (LayerPtrs::sq etc.): the GEMV input is x * g, and the leader's statistics
+// are applied to the row sums in the epilogue, so they are computed while the
+// GEMV waves run instead of before.
 template <class C>
 __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int gw, int lane, int len, int NCH,
                                           int items, unsigned tag, uint32_t tok) {
@@ -666,15 +741,20 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   const int wg = blockIdx.x;
   unsigned gen = 0, seq = 0;
   const int pos = len - 1;
-  // embedding (gpt2.rs:377-384): every workgroup computes x0 itself
-  if (leader) {
-    PK_TRACE(p, 0, lane);
-    for (int i = lane; i < D; i += 64) {
+  // embedding (gpt2.rs:377-384): every workgroup computes x0 itself, each
+  // glue wave a third of it
+  if (leader) PK_TRACE(p, 0, lane);
+  {
+    const float* g1 = PK_C(LayerPtrs, p.layers)[0].ln1w;
+    for (int i = gl; i < D; i += NGLUE * 64) {
       float w;
       if (C::WT == W_F32) w = PK_G(float, p.wte)[(long)tok * D + i];
       else w = __uint_as_float((uint32_t)PK_G(uint16_t, p.wte)[(long)tok * D + i] << 16);
-      sm.xraw[i] = w + PK_G(float, p.wpe)[(long)pos * D + i];
+      const float x = w + PK_G(float, p.wpe)[(long)pos * D + i];
+      sm.xraw[i] = x;
+      sm.in_vec[1][i] = x * PK_G(float, g1)[i];
     }
+    glue_input_done(sm, PH_QKV, lane);
   }
   const int item = wg < items ? wg : -1;
   const int ih = item >= 0 ? item / NCH : 0, ic = item >= 0 ? item - ih * NCH : 0;
@@ -696,120 +776,116 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   for (int l = 0; l < p.L; ++l) {
     const __attribute__((address_space(4))) LayerPtrs& LP = PK_C(LayerPtrs, p.layers)[l];
     u64* T = p.tag + (long)l * p.lw;
-    // ---- QKV: LN1(x) @ c_attn + bias; k/v of the new token into the cache ----
     const int tb = 1 + 16 * l;  // trace index base of this layer
-    // parameters of this phase, loaded before waiting for its input
-    LnParams<D> lnq;
-    float bias = 0.f;
-    if (leader) {
-      ln_prefetch<D>(lnq, LP.ln1w, LP.ln1b, lane);
+    float mean = 0.f, inv_std = 0.f;
+    // ---- QKV: LN1(x) @ c_attn + bias; k/v of the new token into the cache ----
+    {
+      // the leader's epilogue constants, loaded before waiting for the input
       const int row0 = wg * GQ::RPW, rows_here = min(GQ::RPW, GQ::N - row0);
-      if (lane < rows_here) bias = PK_G(float, LP.bqkv)[row0 + lane];
-    }
-    if (l > 0) {
-      glue_fetch<GM::RPW, GM::SW>(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
-      glue_barrier(sm, gen, lane, p.err);
-    }
-    if (leader) {
-      PK_TRACE(p, tb + 0, lane);
-      leader_layernorm<D>(sm.xraw, lnq, p.eps, sm.in_vec[1], lane);
-      PK_TRACE(p, 803 + 4 * l, lane);
-      leader_run_gemv(sm, seq, lane, p.err);
-      PK_TRACE(p, tb + 1, lane);
-      const int row0 = wg * GQ::RPW, rows_here = min(GQ::RPW, GQ::N - row0);
-      float* kl = p.kc + (long)l * p.kv_layer;
-      float* vl = p.vc + (long)l * p.kv_layer;
-      for (int lr = lane; lr < rows_here; lr += 64) {
-        const int n = row0 + lr;
-        const float v = row_acc<GQ>(sm, lr) + bias;
-        tstore(T + p.o_qkv + wg * GQ::SW + lr, v, tag);
-        if (n >= D) {
-          const int c = n < 2 * D ? n - D : n - 2 * D;
-          const int h = c / HD, dd = c - h * HD;
-          float* base = n < 2 * D ? kl : vl;
-          PK_GW(float, base)[((long)h * p.P + pos) * HD + dd] = v;
-        }
+      float sr = 0.f, cr = 0.f;
+      if (leader && lane < rows_here) {
+        sr = PK_G(float, LP.sq)[row0 + lane];
+        cr = PK_G(float, LP.cq)[row0 + lane];
       }
-      PK_TRACE(p, tb + 2, lane);
+      if (l > 0) {
+        glue_fetch<GM::RPW, GM::SW, D, true>(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err,
+                                          sm.in_vec[1], LP.ln1w);
+        glue_input_done(sm, PH_QKV, lane);
+      }
+      if (leader) {
+        ++seq;
+        lds_wait_ge(&sm.in_ready[PH_QKV], (unsigned)(l + 1) * NGLUE, p.err);
+        PK_TRACE(p, tb + 0, lane);
+        leader_ln_stats<D>(sm.xraw, p.eps, mean, inv_std, lane);
+        PK_TRACE(p, 803 + 4 * l, lane);
+        lds_wait_ge(&sm.gemv_done, seq * NC, p.err);
+        PK_TRACE(p, tb + 1, lane);
+        float* kl = p.kc + (long)l * p.kv_layer;
+        float* vl = p.vc + (long)l * p.kv_layer;
+        if (lane < rows_here) {
+          const int n = row0 + lane;
+          const float v = inv_std * (row_acc<GQ>(sm, lane) - mean * sr) + cr;
+          tstore(T + p.o_qkv + wg * GQ::SW + lane, v, tag);
+          if (n >= D) {
+            const int c = n < 2 * D ? n - D : n - 2 * D;
+            const int h = c / HD, dd = c - h * HD;
+            float* base = n < 2 * D ? kl : vl;
+            PK_GW(float, base)[((long)h * p.P + pos) * HD + dd] = v;
+          }
+        }
+        PK_TRACE(p, tb + 2, lane);
+      }
     }
     // ---- attention (multi_head_attention_cached, gpt2.rs:772-834): one item
-    //      per workgroup = head ih, positions [j0, j1) ----
-    if (item >= 0) {
-      if (leader) {
-        // q, k_new, v_new of head ih: all three loads in flight, then re-poll
-        const u64* q = T + p.o_qkv + slot_of<GQ::RPW, GQ::SW>(ih * HD + lane);
-        const u64* k = T + p.o_qkv + slot_of<GQ::RPW, GQ::SW>(D + ih * HD + lane);
-        const u64* v = T + p.o_qkv + slot_of<GQ::RPW, GQ::SW>(2 * D + ih * HD + lane);
-        u64 wq = tload(q), wk = tload(k), wv = tload(v);
-        unsigned spins = 0;
-        while ((unsigned)(wq >> 32) != tag || (unsigned)(wk >> 32) != tag || (unsigned)(wv >> 32) != tag) {
-          if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(p.err))) {
-            raise_err(p.err, 1u);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-          if ((unsigned)(wq >> 32) != tag) wq = tload(q);
-          if ((unsigned)(wk >> 32) != tag) wk = tload(k);
-          if ((unsigned)(wv >> 32) != tag) wv = tload(v);
-        }
-        sm.att_q[lane] = __uint_as_float((unsigned)wq);
-        sm.att_k[lane] = __uint_as_float((unsigned)wk);
-        sm.att_v[lane] = __uint_as_float((unsigned)wv);
-        PK_TRACE(p, tb + 3, lane);
+    //      per workgroup = head ih, positions [j0, j1), on the helpers ----
+    if (item >= 0 && leader) {
+      // q, k_new, v_new of head ih (one word per lane each), polled by the
+      // leader and handed to the helpers through LDS
+      float qkv[3];
+      const int idx[3] = {slot_of<GQ::RPW, GQ::SW>(ih * HD + lane), slot_of<GQ::RPW, GQ::SW>(D + ih * HD + lane),
+                          slot_of<GQ::RPW, GQ::SW>(2 * D + ih * HD + lane)};
+      poll_words<3>(T + p.o_qkv, idx, 3, tag, qkv, p.err);
+      sm.att_q[lane] = qkv[0];
+      sm.att_k[lane] = qkv[1];
+      sm.att_v[lane] = qkv[2];
+      lds_release();
+      if (lane == 0) lds_add(&sm.att_go, 1);
+      PK_TRACE(p, tb + 3, lane);
+    }
+    if (item >= 0 && !leader) {
+      const int grp = lane >> 4, dq = (lane & 15) * 4;
+      lds_wait_ge(&sm.att_go, (unsigned)(l + 1), p.err);
+      if (gw == 1) PK_TRACE(p, 801 + 4 * l, lane);
+      const float* Kh = p.kc + (long)l * p.kv_layer + kv_head;
+      const float* Vh = p.vc + (long)l * p.kv_layer + kv_head;
+      const float4 q4 = *reinterpret_cast<const float4*>(sm.att_q + dq);
+      float m = -INFINITY, lsum = 0.f;
+      float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int w0 = h0; w0 < h1; w0 += KVW) {
+        const int n = min(KVW, h1 - w0);
+        if (w0 > h0) stage_rows(Kh, Vh, w0, n, ldsK, ldsV, lane);  // windows after the first
+        wait_vm_all();
+        att_window(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
       }
-      glue_barrier(sm, gen, lane, p.err);
-      if (!leader) {
-        if (gw == 1) PK_TRACE(p, 801 + 4 * l, lane);
-        const float* Kh = p.kc + (long)l * p.kv_layer + kv_head;
-        const float* Vh = p.vc + (long)l * p.kv_layer + kv_head;
-        const int grp = lane >> 4, dq = (lane & 15) * 4;
-        const float4 q4 = *reinterpret_cast<const float4*>(sm.att_q + dq);
-        float m = -INFINITY, lsum = 0.f;
-        float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int w0 = h0; w0 < h1; w0 += KVW) {
-          const int n = min(KVW, h1 - w0);
-          if (w0 > h0) stage_rows(Kh, Vh, w0, n, ldsK, ldsV, lane);  // windows after the first
-          wait_vm_all();
-          att_window(ldsK, ldsV, n, q4, grp, dq, m, lsum, o4);
-        }
-        if (has_new) {  // row pos: k/v of the new token, counted once (row group 0)
-          const float4 k = *reinterpret_cast<const float4*>(sm.att_k + dq);
-          const float4 v = *reinterpret_cast<const float4*>(sm.att_v + dq);
-          const float s = row16_sum(q4.x * k.x + q4.y * k.y + q4.z * k.z + q4.w * k.w) * 0.125f;
-          const float mn = fmaxf(m, s);
-          const float corr = m == -INFINITY ? 0.f : expf(m - mn);
-          const float pj = grp == 0 ? expf(s - mn) : 0.f;
-          lsum = lsum * corr + pj;
-          o4.x = o4.x * corr + pj * v.x;
-          o4.y = o4.y * corr + pj * v.y;
-          o4.z = o4.z * corr + pj * v.z;
-          o4.w = o4.w * corr + pj * v.w;
-          m = mn;
-        }
-        // sum over the 4 row groups
-        lsum = xor32_sum(xor16_sum(lsum));
-        o4.x = xor32_sum(xor16_sum(o4.x));
-        o4.y = xor32_sum(xor16_sum(o4.y));
-        o4.z = xor32_sum(xor16_sum(o4.z));
-        o4.w = xor32_sum(xor16_sum(o4.w));
-        if (lane < 16) {
-          sm.att_part[hw][2 + dq + 0] = o4.x;
-          sm.att_part[hw][2 + dq + 1] = o4.y;
-          sm.att_part[hw][2 + dq + 2] = o4.z;
-          sm.att_part[hw][2 + dq + 3] = o4.w;
-        }
-        if (lane == 0) {
-          sm.att_part[hw][0] = m;  // -inf (and lsum 0) when this helper had no rows
-          sm.att_part[hw][1] = lsum;
-        }
-        if (gw == 1) PK_TRACE(p, 802 + 4 * l, lane);
+      if (has_new) {  // row pos: k/v of the new token, counted once (row group 0)
+        const float4 k = *reinterpret_cast<const float4*>(sm.att_k + dq);
+        const float4 v = *reinterpret_cast<const float4*>(sm.att_v + dq);
+        const float s = row16_sum(q4.x * k.x + q4.y * k.y + q4.z * k.z + q4.w * k.w) * 0.125f;
+        const float mn = fmaxf(m, s);
+        const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+        const float pj = grp == 0 ? expf(s - mn) : 0.f;
+        lsum = lsum * corr + pj;
+        o4.x = o4.x * corr + pj * v.x;
+        o4.y = o4.y * corr + pj * v.y;
+        o4.z = o4.z * corr + pj * v.z;
+        o4.w = o4.w * corr + pj * v.w;
+        m = mn;
       }
-      glue_barrier(sm, gen, lane, p.err);
-      if (!leader && l + 1 < p.L && h1 > h0) {  // the window is free again: load the next layer's first one
-        const long nl = (long)(l + 1) * p.kv_layer + kv_head;
-        stage_rows(p.kc + nl, p.vc + nl, h0, min(KVW, h1 - h0), ldsK, ldsV, lane);
+      // sum over the 4 row groups
+      lsum = xor32_sum(xor16_sum(lsum));
+      o4.x = xor32_sum(xor16_sum(o4.x));
+      o4.y = xor32_sum(xor16_sum(o4.y));
+      o4.z = xor32_sum(xor16_sum(o4.z));
+      o4.w = xor32_sum(xor16_sum(o4.w));
+      if (lane < 16) {
+        sm.att_part[hw][2 + dq + 0] = o4.x;
+        sm.att_part[hw][2 + dq + 1] = o4.y;
+        sm.att_part[hw][2 + dq + 2] = o4.z;
+        sm.att_part[hw][2 + dq + 3] = o4.w;
       }
-      if (leader) {  // merge the helpers' (m, l, o) into the item's partial softmax
+      if (lane == 0) {
+        sm.att_part[hw][0] = m;  // -inf (and lsum 0) when this helper had no rows
+        sm.att_part[hw][1] = lsum;
+      }
+      if (gw == 1) PK_TRACE(p, 802 + 4 * l, lane);
+      // the helper that finishes last merges the helpers' (m, l, o) into the
+      // item's partial softmax and publishes it
+      lds_release();
+      unsigned arrived = 0;
+      if (lane == 0) arrived = __hip_atomic_fetch_add(&sm.att_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      arrived = __builtin_amdgcn_readlane(arrived, 0);
+      if (arrived == (unsigned)((l + 1) * NA - 1)) {
+        lds_acquire();
         PK_TRACE(p, tb + 4, lane);
         float M = -INFINITY;
         for (int w = 0; w < NA; ++w) M = fmaxf(M, sm.att_part[w][0]);
@@ -834,110 +910,124 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
           }
         }
       }
+      if (l + 1 < p.L && h1 > h0) {  // the window is free again: load the next layer's first one
+        const long nl = (long)(l + 1) * p.kv_layer + kv_head;
+        stage_rows(p.kc + nl, p.vc + nl, h0, min(KVW, h1 - h0), ldsK, ldsV, lane);
+      }
     }
     // ---- attention projection + residual (gpt2.rs:523-526) ----
-    if (leader) {
+    {
       const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
-      bias = lane < rows_here ? PK_G(float, LP.baproj)[row0 + lane] : 0.f;
-    }
-    if (NCH == 1) {
-      // one item per head: the heads' outputs are the projection input
-      glue_fetch<HD, ITEM_SLOT>(T + p.o_att, H * HD, tag, sm.in_vec[0], gl, p.err);
-      if (leader) PK_TRACE(p, tb + 14, lane);
-    } else {
-      glue_fetch<ITEM_WORDS, ITEM_SLOT>(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
-      if (leader) PK_TRACE(p, tb + 14, lane);
-      glue_barrier(sm, gen, lane, p.err);
-      // merge the chunks of each head; heads are spread over the glue waves
-      for (int h = gw; h < H; h += NGLUE) {
-        float M = -INFINITY;
-        for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS + HD]);
-        float Ls = 0.f, o = 0.f;
-        for (int c = 0; c < NCH; ++c) {
-          const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
-          if (it[HD] == -INFINITY) continue;
-          const float f = expf(it[HD] - M);
-          Ls += it[HD + 1] * f;
-          o += it[lane] * f;
+      const float bias = leader && lane < rows_here ? PK_G(float, LP.baproj)[row0 + lane] : 0.f;
+      if (NCH == 1) {
+        // one item per head: the heads' outputs are the projection input
+        glue_fetch<HD, ITEM_SLOT, H * HD>(T + p.o_att, H * HD, tag, sm.in_vec[0], gl, p.err);
+      } else {
+        glue_fetch<ITEM_WORDS, ITEM_SLOT, 8 * NGLUE * 64>(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
+        glue_barrier(sm, gen, lane, p.err);
+        // merge the chunks of each head; heads are spread over the glue waves
+        for (int h = gw; h < H; h += NGLUE) {
+          float M = -INFINITY;
+          for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS + HD]);
+          float Ls = 0.f, o = 0.f;
+          for (int c = 0; c < NCH; ++c) {
+            const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
+            if (it[HD] == -INFINITY) continue;
+            const float f = expf(it[HD] - M);
+            Ls += it[HD + 1] * f;
+            o += it[lane] * f;
+          }
+          sm.in_vec[0][h * HD + lane] = o / Ls;
         }
-        sm.in_vec[0][h * HD + lane] = o / Ls;
+      }
+      glue_input_done(sm, PH_PROJ, lane);
+      if (leader) {
+        PK_TRACE(p, tb + 5, lane);
+        lds_wait_ge(&sm.gemv_done, ++seq * NC, p.err);
+        PK_TRACE(p, tb + 6, lane);
+        if (lane < rows_here)
+          tstore(T + p.o_x2 + wg * GP::SW + lane, sm.xraw[row0 + lane] + (row_acc<GP>(sm, lane) + bias), tag);
+        PK_TRACE(p, tb + 7, lane);
       }
     }
-    glue_barrier(sm, gen, lane, p.err);
-    if (leader) {
-      PK_TRACE(p, tb + 5, lane);
-      leader_run_gemv(sm, seq, lane, p.err);
-      PK_TRACE(p, tb + 6, lane);
-      const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
-      for (int lr = lane; lr < rows_here; lr += 64) {
-        const int n = row0 + lr;
-        tstore(T + p.o_x2 + wg * GP::SW + lr, sm.xraw[n] + (row_acc<GP>(sm, lr) + bias), tag);
-      }
-      PK_TRACE(p, tb + 7, lane);
-    }
-    // ---- FC + gelu_new (gpt2.rs:529-533) ----
-    if (leader) {
-      ln_prefetch<D>(lnq, LP.ln2w, LP.ln2b, lane);
+    // ---- FC + gelu_new (gpt2.rs:529-533), LN2 folded ----
+    {
       const int row0 = wg * GF::RPW, rows_here = min(GF::RPW, GF::N - row0);
-      bias = lane < rows_here ? PK_G(float, LP.bfc)[row0 + lane] : 0.f;
-    }
-    glue_fetch<GP::RPW, GP::SW>(T + p.o_x2, D, tag, sm.x2raw, gl, p.err);
-    glue_barrier(sm, gen, lane, p.err);
-    if (leader) {
-      PK_TRACE(p, tb + 8, lane);
-      leader_layernorm<D>(sm.x2raw, lnq, p.eps, sm.in_vec[1], lane);
-      leader_run_gemv(sm, seq, lane, p.err);
-      PK_TRACE(p, tb + 9, lane);
-      const int row0 = wg * GF::RPW, rows_here = min(GF::RPW, GF::N - row0);
-      for (int lr = lane; lr < rows_here; lr += 64) {
-        const int n = row0 + lr;
-        tstore(T + p.o_h + wg * GF::SW + lr, gelu_new(row_acc<GF>(sm, lr) + bias), tag);
+      float sr = 0.f, cr = 0.f;
+      if (leader && lane < rows_here) {
+        sr = PK_G(float, LP.sf)[row0 + lane];
+        cr = PK_G(float, LP.cf)[row0 + lane];
       }
-      PK_TRACE(p, tb + 10, lane);
+      glue_fetch<GP::RPW, GP::SW, D, true>(T + p.o_x2, D, tag, sm.x2raw, gl, p.err, sm.in_vec[1], LP.ln2w);
+      glue_input_done(sm, PH_FC, lane);
+      if (leader) {
+        ++seq;
+        lds_wait_ge(&sm.in_ready[PH_FC], (unsigned)(l + 1) * NGLUE, p.err);
+        PK_TRACE(p, tb + 8, lane);
+        leader_ln_stats<D>(sm.x2raw, p.eps, mean, inv_std, lane);
+        PK_TRACE(p, 800 + 4 * l, lane);
+        lds_wait_ge(&sm.gemv_done, seq * NC, p.err);
+        PK_TRACE(p, tb + 9, lane);
+        if (lane < rows_here)
+          tstore(T + p.o_h + wg * GF::SW + lane, gelu_new(inv_std * (row_acc<GF>(sm, lane) - mean * sr) + cr), tag);
+        PK_TRACE(p, tb + 10, lane);
+      }
     }
     // ---- MLP projection + residual (gpt2.rs:534-537) ----
-    if (leader) {
+    {
       const int row0 = wg * GM::RPW, rows_here = min(GM::RPW, GM::N - row0);
-      bias = lane < rows_here ? PK_G(float, LP.bmproj)[row0 + lane] : 0.f;
-    }
-    glue_fetch<GF::RPW, GF::SW>(T + p.o_h, 4 * D, tag, sm.in_vec[0], gl, p.err);
-    if (leader) PK_TRACE(p, tb + 15, lane);
-    glue_barrier(sm, gen, lane, p.err);
-    if (leader) {
-      PK_TRACE(p, tb + 11, lane);
-      leader_run_gemv(sm, seq, lane, p.err);
-      PK_TRACE(p, tb + 12, lane);
-      const int row0 = wg * GM::RPW, rows_here = min(GM::RPW, GM::N - row0);
-      for (int lr = lane; lr < rows_here; lr += 64) {
-        const int n = row0 + lr;
-        tstore(T + p.o_x3 + wg * GM::SW + lr, sm.x2raw[n] + (row_acc<GM>(sm, lr) + bias), tag);
+      const float bias = leader && lane < rows_here ? PK_G(float, LP.bmproj)[row0 + lane] : 0.f;
+      // at most 16 words per lane in flight (more spills registers at the
+      // larger widths): 3072 words per polling round
+      glue_fetch<GF::RPW, GF::SW, (4 * D < 3072 ? 4 * D : 3072)>(T + p.o_h, 4 * D, tag, sm.in_vec[0], gl, p.err);
+      glue_input_done(sm, PH_MLP, lane);
+      if (leader) {
+        PK_TRACE(p, tb + 15, lane);
+        lds_wait_ge(&sm.gemv_done, ++seq * NC, p.err);
+        PK_TRACE(p, tb + 12, lane);
+        if (lane < rows_here)
+          tstore(T + p.o_x3 + wg * GM::SW + lane, sm.x2raw[row0 + lane] + (row_acc<GM>(sm, lane) + bias), tag);
+        PK_TRACE(p, tb + 13, lane);
       }
-      PK_TRACE(p, tb + 13, lane);
     }
   }
-  // ---- ln_f + tied LM head + argmax (gpt2.rs:392-396, 858-868) ----
-  LnParams<D> lnf;
-  if (leader) ln_prefetch<D>(lnf, p.lnfw, p.lnfb, lane);
-  glue_fetch<GM::RPW, GM::SW>(p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err);
-  glue_barrier(sm, gen, lane, p.err);
+  // ---- ln_f + tied LM head + argmax (gpt2.rs:392-396, 858-868), ln_f folded ----
+  constexpr int NLR = (GL::RPW + 63) / 64;  // LM-head rows per leader lane
+  const int row0 = wg * GL::RPW, rows_here = min(GL::RPW, GL::N - row0);
+  float sl[NLR], cl[NLR];
+#pragma unroll
+  for (int k = 0; k < NLR; ++k) {
+    const int lr = lane + 64 * k;
+    sl[k] = leader && lr < rows_here ? PK_G(float, p.sl)[row0 + lr] : 0.f;
+    cl[k] = leader && lr < rows_here ? PK_G(float, p.cl)[row0 + lr] : 0.f;
+  }
+  glue_fetch<GM::RPW, GM::SW, D, true>(p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err,
+                                    sm.in_vec[1], p.lnfw);
+  glue_input_done(sm, PH_LM, lane);
   if (leader) {
+    ++seq;
+    lds_wait_ge(&sm.in_ready[PH_LM], NGLUE, p.err);
     PK_TRACE(p, 1 + 16 * p.L, lane);
-    leader_layernorm<D>(sm.xraw, lnf, p.eps, sm.in_vec[1], lane);
-    leader_run_gemv(sm, seq, lane, p.err);
+    float mean, inv_std;
+    leader_ln_stats<D>(sm.xraw, p.eps, mean, inv_std, lane);
+    lds_wait_ge(&sm.gemv_done, seq * NC, p.err);
     PK_TRACE(p, 2 + 16 * p.L, lane);
-    const int row0 = wg * GL::RPW, rows_here = min(GL::RPW, GL::N - row0);
     u64 best = 0ull;
-    for (int lr = lane; lr < rows_here; lr += 64) {
-      const int n = row0 + lr;
-      const float v = row_acc<GL>(sm, lr);
-      PK_GW(float, p.logits)[n] = v;
-      u64 k = 0ull;
-      if (v > -INFINITY) {  // -inf and NaN never win (strict '>' from -inf)
-        uint32_t b = __float_as_uint(v);
-        b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-        k = ((u64)b << 32) | (u64)(~(uint32_t)n);
+#pragma unroll
+    for (int k = 0; k < NLR; ++k) {
+      const int lr = lane + 64 * k;
+      if (lr < rows_here) {
+        const int n = row0 + lr;
+        const float v = inv_std * (row_acc<GL>(sm, lr) - mean * sl[k]) + cl[k];
+        PK_GW(float, p.logits)[n] = v;
+        u64 key = 0ull;
+        if (v > -INFINITY) {  // -inf and NaN never win (strict '>' from -inf)
+          uint32_t b = __float_as_uint(v);
+          b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+          key = ((u64)b << 32) | (u64)(~(uint32_t)n);
+        }
+        best = key > best ? key : best;
       }
-      best = k > best ? k : best;
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -992,7 +1082,9 @@ __global__ __launch_bounds__(NTHREADS) void decode_step_kernel(Params p) {
   __shared__ Smem<D> sm;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (threadIdx.x == 0) {
-    sm.gemv_ready = 0;
+    for (int i = 0; i < 5; ++i) sm.in_ready[i] = 0;
+    sm.att_go = 0;
+    sm.att_cnt = 0;
     sm.gemv_done = 0;
     sm.glue_cnt = 0;
     sm.trace_t0 = wall_clock64();
