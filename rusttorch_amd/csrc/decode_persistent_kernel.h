@@ -18,8 +18,9 @@
 //    overwritten while someone may still read it.
 //  * Waves are specialised so that no wave holding in-flight weight loads
 //    ever has to drain them for a publication:
-//      wave 0         leader: LayerNorm, attention merge, epilogues, stores
-//      waves 1..NA    helpers: poll inputs with the leader; attention
+//      wave 0         leader: LayerNorm statistics, epilogues, stores;
+//                     polls the attention's q/k/v; attention rows
+//      waves 1..NA    helpers: poll inputs with the leader; attention rows
 //      waves NA+1..   GEMV waves: weights in registers, dot products
 //    Leader/helpers and GEMV waves meet only through LDS counters, and all
 //    pointers are address-space qualified so no flat access ties the LDS
@@ -41,6 +42,7 @@ constexpr int G = 256;              // workgroups = CUs of an MI355X
 constexpr int NA = 2;               // helper waves
 constexpr int NC = 5;               // GEMV waves
 constexpr int NGLUE = 1 + NA;       // leader + helpers
+constexpr int NATT = NGLUE;         // attention waves: the leader and the helpers
 constexpr int NTHREADS = (1 + NA + NC) * 64;
 constexpr int HD = 64;              // head_dim of every GPT-2 size
 constexpr int CMAX = 16;            // attention chunks per head
@@ -52,7 +54,7 @@ constexpr int PART_MAX = 1536;      // segment partials per workgroup
 // every supported shape, so no wave can run a whole layer ahead of another and
 // a count of NGLUE * (l + 1) means that every glue wave delivered layer l.
 enum { PH_QKV = 0, PH_PROJ = 1, PH_FC = 2, PH_MLP = 3, PH_LM = 4 };
-constexpr int KVS = 128;            // cached positions of one item staged in LDS
+constexpr int KVS = 120;            // cached positions of one item staged in LDS (NATT windows)
 // Exchange layout: each producer owns a slot of whole 128-byte lines, so no
 // two producers ever write the same line and readers of one producer's words
 // touch only that producer's lines (lines written by many producers and read
@@ -160,13 +162,13 @@ struct Smem {
   float part[PART_MAX];
   float stage[MAX_ITEMS * ITEM_WORDS];
   float kv_k[KVS * HD], kv_v[KVS * HD];  // K/V rows [j0, j0 + KVS) of this workgroup's item
-  float att_part[NA][ITEM_WORDS];
+  float att_part[NATT][ITEM_WORDS];
   float att_q[HD], att_k[HD], att_v[HD];
   // in_ready[phase]: +1 per glue wave once its share of that phase's GEMV
   // input is in LDS (one counter per phase type, see PH_QKV..PH_LM);
   // gemv_done: +1 per GEMV wave per phase; glue_cnt: glue-wave barrier;
-  // att_go: layers whose q/k/v the leader has put in LDS; att_cnt: helpers
-  // that finished the layer's attention.
+  // att_go: layers whose q/k/v the leader has put in LDS; att_cnt: attention
+  // waves that finished the layer's attention.
   unsigned in_ready[5], gemv_done, glue_cnt, att_go, att_cnt;
   u64 trace_t0;
   unsigned trace_rel[TRACE_N];
@@ -596,13 +598,16 @@ __device__ __forceinline__ void leader_ln_stats(const float* src, float eps, flo
 }
 
 // ---------------------------------------------------------------------------
-// Attention of one item on the helper waves. Helper hw owns cached rows
+// Attention of one item on the NATT glue waves. Wave hw owns cached rows
 // [h0, h1) of the item's head and processes them in windows of KVW rows held
 // in its own part of the LDS stage.
 // ---------------------------------------------------------------------------
-constexpr int KVW = KVS / NA;  // rows of one helper's LDS window
+constexpr int KVW = KVS / NATT;  // rows of one attention wave's LDS window
+// stage_rows fills a window in groups of 4 rows (one 1-KiB LDS-DMA
+// instruction each), so a window must hold a whole number of groups
+static_assert(KVW % 4 == 0 && KVW * NATT == KVS, "attention window");
 
-// Copy K/V rows [r0, r0 + n), n <= KVW, into a helper's LDS window with
+// Copy K/V rows [r0, r0 + n), n <= KVW, into a wave's LDS window with
 // LDS-direct loads (global_load_lds_dwordx4: lane i of an instruction fills
 // bytes [16i, 16i + 16) after the wave-uniform LDS address), so no registers
 // are held while the rows are in flight; the wave's own s_waitcnt vmcnt(0)
@@ -631,7 +636,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // Online-softmax update of (m, lsum, o4) with the n rows (1 <= n <= KVW) of a
-// helper's LDS window (gpt2.rs:796-830: scores q.k / sqrt(64), softmax, p.V).
+// wave's LDS window (gpt2.rs:796-830: scores q.k / sqrt(64), softmax, p.V).
 // 16 lanes per row (4 dims each), 4 rows per wave instruction; lane (grp, dq)
 // accumulates lsum and o4 over rows 4t + grp, summed over grp by the caller.
 // AT row groups of 4 (n <= 4 * AT); straight-line code so that all LDS reads
@@ -760,18 +765,18 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   const int ih = item >= 0 ? item / NCH : 0, ic = item >= 0 ? item - ih * NCH : 0;
   const int CL = (len + NCH - 1) / NCH;
   const int j0 = ic * CL, j1 = min(len, j0 + CL);
-  // Helper rows: the cached rows [j0, min(j1, pos)) of the item are split
-  // between the helpers; the new row pos (when in the item) goes to the last
-  // helper. Cached rows are final at step start, so each helper loads its
-  // first window of a layer into LDS long before the layer's q is known.
-  const int hw = gw > 0 ? gw - 1 : 0;
-  const int cend = min(j1, pos), per = (cend - j0 + NA - 1) / NA;
+  // Attention rows: the cached rows [j0, min(j1, pos)) of the item are split
+  // between the NATT glue waves; the new row pos (when in the item) goes to
+  // the last helper. Cached rows are final at step start, so each wave loads
+  // its first window of a layer into LDS long before the layer's q is known.
+  const int hw = gw;
+  const int cend = min(j1, pos), per = (cend - j0 + NATT - 1) / NATT;
   const int h0 = min(cend, j0 + hw * per), h1 = min(cend, h0 + per);
-  const bool has_new = hw == NA - 1 && j1 == len;
+  const bool has_new = hw == NATT - 1 && j1 == len;
   float* ldsK = sm.kv_k + hw * KVW * HD;
   float* ldsV = sm.kv_v + hw * KVW * HD;
   const long kv_head = (long)ih * p.P * HD;
-  if (item >= 0 && !leader && h1 > h0)
+  if (item >= 0 && h1 > h0)
     stage_rows(p.kc + kv_head, p.vc + kv_head, h0, min(KVW, h1 - h0), ldsK, ldsV, lane);
   for (int l = 0; l < p.L; ++l) {
     const __attribute__((address_space(4))) LayerPtrs& LP = PK_C(LayerPtrs, p.layers)[l];
@@ -817,7 +822,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       }
     }
     // ---- attention (multi_head_attention_cached, gpt2.rs:772-834): one item
-    //      per workgroup = head ih, positions [j0, j1), on the helpers ----
+    //      per workgroup = head ih, positions [j0, j1), on the glue waves ----
     if (item >= 0 && leader) {
       // q, k_new, v_new of head ih (one word per lane each), polled by the
       // leader and handed to the helpers through LDS
@@ -832,9 +837,9 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       if (lane == 0) lds_add(&sm.att_go, 1);
       PK_TRACE(p, tb + 3, lane);
     }
-    if (item >= 0 && !leader) {
+    if (item >= 0) {
       const int grp = lane >> 4, dq = (lane & 15) * 4;
-      lds_wait_ge(&sm.att_go, (unsigned)(l + 1), p.err);
+      if (!leader) lds_wait_ge(&sm.att_go, (unsigned)(l + 1), p.err);
       if (gw == 1) PK_TRACE(p, 801 + 4 * l, lane);
       const float* Kh = p.kc + (long)l * p.kv_layer + kv_head;
       const float* Vh = p.vc + (long)l * p.kv_layer + kv_head;
@@ -874,23 +879,23 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         sm.att_part[hw][2 + dq + 3] = o4.w;
       }
       if (lane == 0) {
-        sm.att_part[hw][0] = m;  // -inf (and lsum 0) when this helper had no rows
+        sm.att_part[hw][0] = m;  // -inf (and lsum 0) when this wave had no rows
         sm.att_part[hw][1] = lsum;
       }
       if (gw == 1) PK_TRACE(p, 802 + 4 * l, lane);
-      // the helper that finishes last merges the helpers' (m, l, o) into the
+      // the wave that finishes last merges the waves' (m, l, o) into the
       // item's partial softmax and publishes it
       lds_release();
       unsigned arrived = 0;
       if (lane == 0) arrived = __hip_atomic_fetch_add(&sm.att_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       arrived = __builtin_amdgcn_readlane(arrived, 0);
-      if (arrived == (unsigned)((l + 1) * NA - 1)) {
+      if (arrived == (unsigned)((l + 1) * NATT - 1)) {
         lds_acquire();
         PK_TRACE(p, tb + 4, lane);
         float M = -INFINITY;
-        for (int w = 0; w < NA; ++w) M = fmaxf(M, sm.att_part[w][0]);
+        for (int w = 0; w < NATT; ++w) M = fmaxf(M, sm.att_part[w][0]);
         float Ls = 0.f, o = 0.f;
-        for (int w = 0; w < NA; ++w) {
+        for (int w = 0; w < NATT; ++w) {
           const float mw = sm.att_part[w][0];
           if (mw == -INFINITY) continue;
           const float f = expf(mw - M);
