@@ -317,8 +317,9 @@ struct V16<W_BF16> {
 // PACE > 0: sleep up to PACE*64 clocks between loads while the wave's next
 // input is not ready yet (*ready < next), so a refill does not flood this
 // CU's memory queue ahead of the exchanges; the sleep is cut short (to 128
-// clocks) once the input is ready, and is the only conditional part: the
-// loads stay in fixed order.
+// clocks) once the input is ready, after which the remaining loads go out
+// back to back. The pacing is the only conditional part: the loads stay in
+// fixed order.
 #ifndef PK_LM_NT
 #define PK_LM_NT 1
 #endif
@@ -337,6 +338,7 @@ __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], co
   const int nseg = min(GEO::SPW, segs_here - s0);
   int lr = s0 / GEO::SPR, j = s0 - lr * GEO::SPR;
   const Vec* base = reinterpret_cast<const Vec*>(W) + (long)row0 * GEO::VR;
+  bool go = false;  // the input was seen ready: no more pacing (nor LDS reads)
   // Branch-free: the compiler's wait-count analysis then sees a fixed load
   // order and waits only for the buffer being consumed. Segments this wave
   // does not own read a small zero page instead (L2-resident).
@@ -349,8 +351,14 @@ __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], co
       // streaming bandwidth than plain loads on this part)
       if constexpr (NT) buf[i] = __builtin_nontemporal_load(PK_G(Vec, rowp) + li);
       else buf[i] = PK_G(Vec, rowp)[li];
-      if (PACE > 0 && i + 1 < GEO::SPW)
-        for (int t = 0; t < PACE / 2 && lds_load(ready) < next; ++t) __builtin_amdgcn_s_sleep(2);
+      if (PACE > 0 && i + 1 < GEO::SPW && !go)
+        for (int t = 0; t < PACE / 2; ++t) {
+          if (lds_load(ready) >= next) {
+            go = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
     }
     if (++j == GEO::SPR) {
       j = 0;
