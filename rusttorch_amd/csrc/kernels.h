@@ -74,7 +74,9 @@ void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past
                          int n_head, int n_pos, int d, float* out);
 
 // bf16 conversion / transposition used once at model load.
-void launch_transpose_to(hipStream_t s, const float* src, int rows, int cols, void* dst, int wtype);
-void launch_convert_to(hipStream_t s, const float* src, long n, void* dst, int wtype);
+// Element types of a source tensor as uploaded from the caller or the file.
+enum { SRC_F32 = 0, SRC_BF16 = 1, SRC_F16 = 2 };
+void launch_transpose_to(hipStream_t s, const void* src, int stype, int rows, int cols, void* dst, int wtype);
+void launch_convert_to(hipStream_t s, const void* src, int stype, long n, void* dst, int wtype);
 
 }  // namespace rtg

@@ -1195,8 +1195,12 @@ void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past
 }
 
 // ---------------------------------------------------------------------------
-// Load-time layout conversion: [rows][cols] f32 -> [cols][rows] f32/bf16
-// (Conv1D [in][out] -> W^T [out][in]), and f32 -> bf16 (round to nearest even).
+// Load-time layout conversion: [rows][cols] -> [cols][rows] (Conv1D [in][out]
+// -> W^T [out][in]) and plain conversion, from the file's element type (f32,
+// bf16 or f16, so that bf16 / f16 weights are uploaded as they are stored and
+// widened here) to the storage type (f32, or bf16 rounded to nearest even).
+// bf16 -> f32 is bf16_to_f32 (bits << 16, nn/safetensors.rs:389-391); f16 ->
+// f32 is the exact IEEE conversion.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -1206,43 +1210,51 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(b >> 16);
 }
 
-__global__ void transpose_kernel(const float* __restrict__ src, int rows, int cols, void* __restrict__ dst,
+__device__ __forceinline__ float load_elem(const void* src, int stype, size_t i) {
+  if (stype == SRC_F32) return static_cast<const float*>(src)[i];
+  const uint16_t h = static_cast<const uint16_t*>(src)[i];
+  if (stype == SRC_BF16) return __uint_as_float((uint32_t)h << 16);
+  _Float16 x;
+  __builtin_memcpy(&x, &h, 2);
+  return (float)x;
+}
+
+__device__ __forceinline__ void store_elem(void* dst, int wtype, size_t i, float v) {
+  if (wtype == W_F32) static_cast<float*>(dst)[i] = v;
+  else static_cast<uint16_t*>(dst)[i] = f32_to_bf16_rne(v);
+}
+
+__global__ void transpose_kernel(const void* __restrict__ src, int stype, int rows, int cols, void* __restrict__ dst,
                                  int wtype) {
   __shared__ float tile[32][33];
   const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
   for (int y = ty; y < 32; y += 8) {
     const int r = r0 + y, c = c0 + tx;
-    tile[y][tx] = (r < rows && c < cols) ? src[(size_t)r * cols + c] : 0.f;
+    tile[y][tx] = (r < rows && c < cols) ? load_elem(src, stype, (size_t)r * cols + c) : 0.f;
   }
   __syncthreads();
   for (int y = ty; y < 32; y += 8) {
     const int c = c0 + y, r = r0 + tx;  // dst[c][r]
-    if (c < cols && r < rows) {
-      const float v = tile[tx][y];
-      if (wtype == W_F32) reinterpret_cast<float*>(dst)[(size_t)c * rows + r] = v;
-      else reinterpret_cast<uint16_t*>(dst)[(size_t)c * rows + r] = f32_to_bf16_rne(v);
-    }
+    if (c < cols && r < rows) store_elem(dst, wtype, (size_t)c * rows + r, tile[tx][y]);
   }
 }
 
-void launch_transpose_to(hipStream_t s, const float* src, int rows, int cols, void* dst, int wtype) {
+void launch_transpose_to(hipStream_t s, const void* src, int stype, int rows, int cols, void* dst, int wtype) {
   dim3 grid((cols + 31) / 32, (rows + 31) / 32);
-  transpose_kernel<<<grid, 256, 0, s>>>(src, rows, cols, dst, wtype);
+  transpose_kernel<<<grid, 256, 0, s>>>(src, stype, rows, cols, dst, wtype);
 }
 
-__global__ void convert_kernel(const float* __restrict__ src, long n, void* __restrict__ dst, int wtype) {
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
-    if (wtype == W_F32) reinterpret_cast<float*>(dst)[i] = src[i];
-    else reinterpret_cast<uint16_t*>(dst)[i] = f32_to_bf16_rne(src[i]);
-  }
+__global__ void convert_kernel(const void* __restrict__ src, int stype, long n, void* __restrict__ dst, int wtype) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    store_elem(dst, wtype, (size_t)i, load_elem(src, stype, (size_t)i));
 }
 
-void launch_convert_to(hipStream_t s, const float* src, long n, void* dst, int wtype) {
+void launch_convert_to(hipStream_t s, const void* src, int stype, long n, void* dst, int wtype) {
   long blocks = (n + 255) / 256;
   if (blocks > 65535) blocks = 65535;
   if (blocks < 1) blocks = 1;
-  convert_kernel<<<(unsigned)blocks, 256, 0, s>>>(src, n, dst, wtype);
+  convert_kernel<<<(unsigned)blocks, 256, 0, s>>>(src, stype, n, dst, wtype);
 }
 
 }  // namespace rtg

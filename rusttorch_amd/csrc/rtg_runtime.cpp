@@ -565,10 +565,20 @@ uint32_t sample_temperature(const float* logits, size_t V, float temperature, Sp
 // ---------------------------------------------------------------------------
 
 namespace {
+// A weight as the caller or the file holds it: f32, bf16 or f16 elements
+// (uploaded as they are and converted on the device), or an f32 decode on the
+// host of any other element type.
 struct HostTensor {
   std::vector<size_t> shape;
-  const float* data = nullptr;
+  const void* data = nullptr;
+  int stype = SRC_F32;
   std::vector<float> owned;
+  size_t numel() const {
+    size_t n = 1;
+    for (size_t x : shape) n *= x;
+    return n;
+  }
+  size_t bytes() const { return numel() * (stype == SRC_F32 ? 4 : 2); }
 };
 
 using Lookup = std::map<std::string, HostTensor>;
@@ -658,17 +668,24 @@ rtg_result build_model(const rtg_config* cfg, Lookup& lk, rtg_storage storage, r
     size_t stage_max = std::max({V * d, P * d, 4 * d * d});
     HIPX(hipMalloc(&staging, stage_max * 4));
     hipStream_t s = nullptr;
+    // Tensors go to the device in their own element type; widening,
+    // narrowing to the storage type and the transpose run there.
     auto upload_f32 = [&](const std::string& nm, size_t off) {
       const auto& t = lk[nm];
-      size_t n = 1;
-      for (size_t x : t.shape) n *= x;
-      HIPX(hipMemcpy(A + off, t.data, n * 4, hipMemcpyHostToDevice));
+      if (t.stype == SRC_F32) {
+        HIPX(hipMemcpy(A + off, t.data, t.bytes(), hipMemcpyHostToDevice));
+        return;
+      }
+      HIPX(hipMemcpy(staging, t.data, t.bytes(), hipMemcpyHostToDevice));
+      launch_convert_to(s, staging, t.stype, (long)t.numel(), A + off, W_F32);
+      HIPX(hipGetLastError());
+      HIPX(hipDeviceSynchronize());
     };
     auto upload_wt = [&](const std::string& nm, size_t off) {  // [K][N] -> W^T [N][K] in storage type
       const auto& t = lk[nm];
       const size_t K = t.shape[0], N = t.shape[1];
-      HIPX(hipMemcpy(staging, t.data, K * N * 4, hipMemcpyHostToDevice));
-      launch_transpose_to(s, staging, (int)K, (int)N, A + off, m->wtype);
+      HIPX(hipMemcpy(staging, t.data, t.bytes(), hipMemcpyHostToDevice));
+      launch_transpose_to(s, staging, t.stype, (int)K, (int)N, A + off, m->wtype);
       HIPX(hipGetLastError());
       HIPX(hipDeviceSynchronize());
     };
@@ -703,8 +720,8 @@ rtg_result build_model(const rtg_config* cfg, Lookup& lk, rtg_storage storage, r
     }
     {
       const auto& t = lk["wte.weight"];
-      HIPX(hipMemcpy(staging, t.data, V * d * 4, hipMemcpyHostToDevice));
-      launch_convert_to(s, staging, (long)(V * d), A + o_wte, m->wtype);
+      HIPX(hipMemcpy(staging, t.data, t.bytes(), hipMemcpyHostToDevice));
+      launch_convert_to(s, staging, t.stype, (long)(V * d), A + o_wte, m->wtype);
       HIPX(hipGetLastError());
       HIPX(hipDeviceSynchronize());
     }
@@ -741,37 +758,15 @@ rtg_result build_model(const rtg_config* cfg, Lookup& lk, rtg_storage storage, r
   return ok();
 }
 
-bool decode_to_f32(const void* data, rtg_dtype dt, size_t n, std::vector<float>* out) {
+bool decode_f64(const void* data, size_t n, std::vector<float>* out) {
   out->resize(n);
   const uint8_t* raw = reinterpret_cast<const uint8_t*>(data);
-  switch (dt) {
-    case RTG_F32: memcpy(out->data(), data, n * 4); return true;
-    case RTG_BF16:
-      for (size_t i = 0; i < n; ++i) {
-        uint32_t b = (uint32_t)(raw[2 * i] | (raw[2 * i + 1] << 8)) << 16;
-        memcpy(&(*out)[i], &b, 4);
-      }
-      return true;
-    case RTG_F64:
-      for (size_t i = 0; i < n; ++i) {
-        double v;
-        memcpy(&v, raw + 8 * i, 8);
-        (*out)[i] = (float)v;
-      }
-      return true;
-    case RTG_F16: {
-      rtg::StFile f;
-      rtg::StEntry e;
-      e.dtype = "F16";
-      e.shape = {n};
-      e.begin = 0;
-      e.end = 2 * n;
-      f.bytes.assign(raw, raw + 2 * n);
-      f.data_start = 0;
-      return rtg::st_decode_f32(f, e, out).empty();
-    }
+  for (size_t i = 0; i < n; ++i) {
+    double v;
+    memcpy(&v, raw + 8 * i, 8);
+    (*out)[i] = (float)v;
   }
-  return false;
+  return true;
 }
 }  // namespace
 
@@ -793,18 +788,19 @@ rtg_result rtg_model_from_host(const rtg_config* cfg, const rtg_named_tensor* te
   Lookup lk;
   for (size_t i = 0; i < n; ++i) {
     const rtg_named_tensor& t = tensors[i];
-    HostTensor h;
+    HostTensor& h = lk[t.name];
     h.shape.assign(t.shape, t.shape + t.ndim);
-    size_t numel = 1;
-    for (size_t s : h.shape) numel *= s;
-    if (t.dtype == RTG_F32) {
-      h.data = reinterpret_cast<const float*>(t.data);
-    } else {
-      if (!decode_to_f32(t.data, t.dtype, numel, &h.owned)) return err("Unsupported dtype for " + std::string(t.name));
-      h.data = h.owned.data();
+    switch (t.dtype) {
+      case RTG_F32: h.stype = SRC_F32; h.data = t.data; break;
+      case RTG_BF16: h.stype = SRC_BF16; h.data = t.data; break;
+      case RTG_F16: h.stype = SRC_F16; h.data = t.data; break;
+      case RTG_F64:
+        decode_f64(t.data, h.numel(), &h.owned);
+        h.stype = SRC_F32;
+        h.data = h.owned.data();
+        break;
+      default: return err("Unsupported dtype for " + std::string(t.name));
     }
-    lk[t.name] = std::move(h);
-    if (lk[t.name].owned.size()) lk[t.name].data = lk[t.name].owned.data();
   }
   return build_model(cfg, lk, storage, out);
 }
@@ -815,17 +811,24 @@ rtg_result rtg_model_from_safetensors(const char* path, const rtg_config* cfg, r
   StFile f;
   std::string e = st_read_file(path, &f);
   if (!e.empty()) return err("Failed to load safetensors: " + e);
+  // F32, BF16 and F16 tensors are used in place in the mapping (no host copy);
+  // other element types are decoded to f32 (safetensors.rs:232-348).
   Lookup lk;
   for (auto& kv : f.entries) {
-    HostTensor h;
-    h.shape = kv.second.shape;
-    e = st_decode_f32(f, kv.second, &h.owned);
+    const StEntry& en = kv.second;
+    HostTensor& h = lk[kv.first];
+    h.shape = en.shape;
+    if (en.dtype == "F32" || en.dtype == "BF16" || en.dtype == "F16") {
+      e = st_check_size(en, en.dtype == "F32" ? 4 : 2, en.dtype.c_str());
+      h.stype = en.dtype == "F32" ? SRC_F32 : en.dtype == "BF16" ? SRC_BF16 : SRC_F16;
+      h.data = st_data(f, en);
+    } else {
+      e = st_decode_f32(f, en, &h.owned);
+      h.stype = SRC_F32;
+      h.data = h.owned.data();
+    }
     if (!e.empty()) return err("Failed to load safetensors: " + e);
-    lk[kv.first] = std::move(h);
-    lk[kv.first].data = lk[kv.first].owned.data();
   }
-  f.bytes.clear();
-  f.bytes.shrink_to_fit();
   return build_model(cfg, lk, storage, out);
 }
 

@@ -1,10 +1,13 @@
 // Minimal safetensors reader; see safetensors_reader.h.
 #include "safetensors_reader.h"
 
+#include <errno.h>
+#include <fcntl.h>
 #include <stdio.h>
 #include <string.h>
-
-#include <fstream>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 namespace rtg {
 namespace {
@@ -171,23 +174,45 @@ float f16_to_f32(uint16_t h) {
 
 }  // namespace
 
+StFile::~StFile() {
+  if (base) munmap(const_cast<uint8_t*>(base), size);
+}
+
+// The file is mapped read-only, not read: tensor bytes go from the page
+// cache to the device (nn/safetensors.rs:94-151 reads it into memory).
 std::string st_read_file(const std::string& path, StFile* out) {
-  std::ifstream in(path, std::ios::binary | std::ios::ate);
-  if (!in) return "I/O error: No such file or directory (os error 2)";
-  std::streamsize sz = in.tellg();
-  in.seekg(0);
-  out->bytes.resize((size_t)sz);
-  if (sz > 0 && !in.read(reinterpret_cast<char*>(out->bytes.data()), sz)) return "I/O error: failed to read " + path;
-  const auto& d = out->bytes;
+  // std::io::Error's Display form, "<strerror> (os error N)"
+  auto io_err = [](int e) { return std::string("I/O error: ") + strerror(e) + " (os error " + std::to_string(e) + ")"; };
+  const int fd = open(path.c_str(), O_RDONLY);
+  if (fd < 0) return io_err(errno);
+  struct stat stt;
+  if (fstat(fd, &stt) != 0) {
+    const int e = errno;
+    close(fd);
+    return io_err(e);
+  }
+  const size_t fsize = (size_t)stt.st_size;
+  if (fsize > 0) {
+    void* m = mmap(nullptr, fsize, PROT_READ, MAP_PRIVATE, fd, 0);
+    if (m == MAP_FAILED) {
+      const int e = errno;
+      close(fd);
+      return io_err(e);
+    }
+    out->base = static_cast<const uint8_t*>(m);
+    out->size = fsize;
+  }
+  close(fd);
+  const uint8_t* d = out->base;
   // safetensors.rs:95-118
-  if (d.size() < 8) return "Invalid safetensors format: File too small — need at least 8 bytes for header size";
+  if (fsize < 8) return "Invalid safetensors format: File too small — need at least 8 bytes for header size";
   uint64_t hs = 0;
   for (int i = 7; i >= 0; --i) hs = (hs << 8) | d[i];
   if (hs == 0) return "Invalid safetensors format: Header size is zero";
-  if (8 + hs > d.size())
-    return "Invalid safetensors format: Header size " + std::to_string(hs) + " exceeds file size " + std::to_string(d.size());
+  if (hs > fsize - 8)
+    return "Invalid safetensors format: Header size " + std::to_string(hs) + " exceeds file size " + std::to_string(fsize);
   out->data_start = 8 + (size_t)hs;
-  Json j{reinterpret_cast<const char*>(d.data()) + 8, reinterpret_cast<const char*>(d.data()) + 8 + hs, {}};
+  Json j{reinterpret_cast<const char*>(d) + 8, reinterpret_cast<const char*>(d) + 8 + hs, {}};
   if (!j.eat('{')) return "Invalid safetensors format: header is not a JSON object";
   if (!j.eat('}')) {
     for (;;) {
@@ -205,7 +230,7 @@ std::string st_read_file(const std::string& path, StFile* out) {
       return "Invalid safetensors format: malformed header";
     }
   }
-  const size_t data_len = d.size() - out->data_start;
+  const size_t data_len = fsize - out->data_start;
   for (auto& kv : out->entries) {
     const StEntry& en = kv.second;
     if (en.end > data_len || en.begin > en.end)
@@ -215,18 +240,22 @@ std::string st_read_file(const std::string& path, StFile* out) {
   return "";
 }
 
+std::string st_check_size(const StEntry& e, size_t elem_bytes, const char* name) {
+  size_t n = 1;
+  for (size_t s : e.shape) n *= s;
+  const size_t len = e.end - e.begin;
+  if (len != n * elem_bytes)
+    return std::string("Invalid safetensors format: ") + name + " tensor: expected " + std::to_string(n * elem_bytes) +
+           " bytes, got " + std::to_string(len);
+  return "";
+}
+
 std::string st_decode_f32(const StFile& f, const StEntry& e, std::vector<float>* out) {
   size_t n = 1;
   for (size_t s : e.shape) n *= s;
-  const uint8_t* raw = f.bytes.data() + f.data_start + e.begin;
-  const size_t len = e.end - e.begin;
+  const uint8_t* raw = st_data(f, e);
   out->resize(n);
-  auto need = [&](size_t w, const char* name) -> std::string {
-    if (len != n * w)
-      return std::string("Invalid safetensors format: ") + name + " tensor: expected " + std::to_string(n * w) + " bytes, got " +
-             std::to_string(len);
-    return "";
-  };
+  auto need = [&](size_t w, const char* name) { return st_check_size(e, w, name); };
   std::string err;
   if (e.dtype == "F32") {
     if (!(err = need(4, "F32")).empty()) return err;

@@ -158,11 +158,20 @@ class Gpt2Model:
         keep = []
         arr = (_lib.NamedTensor * max(1, len(sd)))()
         for i, (name, a) in enumerate(sd.items()):
-            a = np.ascontiguousarray(a, dtype=np.float32)
+            # f16 / f64 arrays go to the library as they are (f16 is widened on
+            # the device); anything else is passed as f32
+            a = np.asarray(a)
+            if a.dtype == np.float16:
+                dt = _lib.RTG_F16
+            elif a.dtype == np.float64:
+                dt = _lib.RTG_F64
+            else:
+                a, dt = a.astype(np.float32, copy=False), _lib.RTG_F32
+            a = np.ascontiguousarray(a)
             shape = (C.c_size_t * max(1, a.ndim))(*a.shape)
             nm = name.encode()
             keep += [a, shape, nm]
-            arr[i] = _lib.NamedTensor(nm, a.ctypes.data, _lib.RTG_F32, a.ndim, shape)
+            arr[i] = _lib.NamedTensor(nm, a.ctypes.data, dt, a.ndim, shape)
         h = C.c_void_p()
         cfg = config._c()
         check(lib.rtg_model_from_host(C.byref(cfg), arr, len(sd), cls._storage(storage), C.byref(h)))

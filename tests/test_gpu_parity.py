@@ -328,3 +328,43 @@ def test_bf16_storage_matches_oracle(O):
     ids = synth.make_tokens(24, sh.vocab_size, stream=5)
     assert_logits_close(m.forward(ids), om.forward(ids), "bf16 forward")
     assert m.generate_cached(ids[:8], 30, 0.0) == om.generate_cached(ids[:8], 30)
+
+
+# ---------------------------------------------------------------------------
+# direct loader: tensors go to the device as stored, converted there
+# (nn/safetensors.rs:94-151 header/offsets, :285-297 BF16, :389-391 bf16_to_f32)
+# ---------------------------------------------------------------------------
+
+def _same_model_outputs(a, b, vocab):
+    ids = synth.make_tokens(12, vocab, stream=7)
+    ca, cb = a.new_cache(), b.new_cache()
+    assert np.array_equal(a.forward_cached(ids, ca), b.forward_cached(ids, cb))
+    for t in (3, 9, 1):
+        assert np.array_equal(a.forward_cached([t], ca), b.forward_cached([t], cb))
+    assert a.generate_cached(ids, 16, 0.0) == b.generate_cached(ids, 16, 0.0)
+
+
+@pytest.mark.parametrize("file_bf16,storage", [(False, "f32"), (True, "bf16"), (True, "f32"), (False, "bf16")])
+def test_safetensors_direct_matches_host(tmp_path, file_bf16, storage):
+    """from_safetensors maps the file and uploads F32 / BF16 tensors as they
+    are stored; widening, rounding to the storage type and the Conv1D
+    transpose run on the device. The model equals from_state_dict on the
+    values the file holds, bit for bit."""
+    sh = synth.SHAPES["mini"]
+    sd = synth.make_weights(sh)
+    path = tmp_path / "m.safetensors"
+    synth.write_safetensors(str(path), sd, bf16=file_bf16)
+    held = {k: synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(v)) for k, v in sd.items()} if file_bf16 else sd
+    a = Gpt2Model.from_safetensors(str(path), cfg_of(sh), storage=storage)
+    b = Gpt2Model.from_state_dict(held, cfg_of(sh), storage=storage)
+    _same_model_outputs(a, b, sh.vocab_size)
+
+
+def test_f16_host_tensors_widened_on_device():
+    """f16 host tensors (rtg_model_from_host with RTG_F16) are widened on the
+    device exactly: the model equals one built from the same values in f32."""
+    sh = synth.SHAPES["mini"]
+    sd16 = {k: v.astype(np.float16) for k, v in synth.make_weights(sh).items()}
+    a = Gpt2Model.from_state_dict(sd16, cfg_of(sh))
+    b = Gpt2Model.from_state_dict({k: v.astype(np.float32) for k, v in sd16.items()}, cfg_of(sh))
+    _same_model_outputs(a, b, sh.vocab_size)
