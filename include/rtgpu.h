@@ -152,6 +152,45 @@ rtg_result rtg_forward_cached_batched(const rtg_model* model, rtg_cache* cache, 
 rtg_result rtg_generate_cached_batched(const rtg_model* model, const uint32_t* prompts, size_t batch, size_t n,
                                        size_t max_new, uint32_t* out, rtg_timing* timing);
 
+/* ---- BpeTokenizer, rusttorch-core/src/data/tokenizer.rs (host-side text in
+ * and out; used by the reference's example at examples/gpt2.rs:77-95).
+ * Text is UTF-8 with an explicit length (a Rust &str). Buffers that a call
+ * returns (ids, text, spans) are owned by the caller and released with
+ * rtg_free_buffer. Errors carry the reference's messages. ---- */
+typedef struct rtg_tokenizer rtg_tokenizer;
+/* BpeTokenizer::from_files, tokenizer.rs:45-53. Errors: "Failed to read
+ * vocab.json: <io error>", "Failed to read merges.txt: <io error>", then those
+ * of from_strings. */
+rtg_result rtg_tokenizer_from_files(const char* vocab_json_path, const char* merges_txt_path, rtg_tokenizer** out);
+/* BpeTokenizer::from_strings, tokenizer.rs:55-82 (parse_vocab_json :356-401,
+ * parse_merges :486-514). */
+rtg_result rtg_tokenizer_from_strings(const char* vocab_json, size_t vocab_len, const char* merges_txt,
+                                      size_t merges_len, rtg_tokenizer** out);
+/* BpeTokenizer::from_vocab_and_merges, tokenizer.rs:186-219: token i gets id
+ * i, merge rule r gets rank r. Strings are NUL-terminated UTF-8. */
+rtg_result rtg_tokenizer_from_vocab_and_merges(const char* const* vocab, size_t n_vocab, const char* const* merge_a,
+                                               const char* const* merge_b, size_t n_merges, rtg_tokenizer** out);
+void rtg_tokenizer_destroy(rtg_tokenizer* t);
+/* BpeTokenizer::encode, tokenizer.rs:85-112: *ids receives *n token ids. */
+rtg_result rtg_tokenizer_encode(const rtg_tokenizer* t, const char* text, size_t len, uint32_t** ids, size_t* n);
+/* BpeTokenizer::decode, tokenizer.rs:115-130: *text receives *len bytes of
+ * UTF-8 (from_utf8_lossy), NUL-terminated. */
+rtg_result rtg_tokenizer_decode(const rtg_tokenizer* t, const uint32_t* ids, size_t n, char** text, size_t* len);
+/* BpeTokenizer::vocab_size / token_to_id / id_to_token, tokenizer.rs:133-145.
+ * id_to_token points *token at the tokenizer's own copy (valid while it
+ * lives); false is Rust's None. */
+size_t rtg_tokenizer_vocab_size(const rtg_tokenizer* t);
+bool rtg_tokenizer_token_to_id(const rtg_tokenizer* t, const char* token, size_t len, uint32_t* id);
+bool rtg_tokenizer_id_to_token(const rtg_tokenizer* t, uint32_t id, const char** token, size_t* len);
+/* pre_tokenize, tokenizer.rs:260-331 (private in the reference; exported for
+ * the parity tests): byte ranges of the words, (*spans)[2k] .. (*spans)[2k+1]. */
+rtg_result rtg_tokenizer_pre_tokenize(const char* text, size_t len, size_t** spans, size_t* n_words);
+/* build_byte_encoder, tokenizer.rs:223-241 (private in the reference;
+ * exported for the parity tests): the code point of every byte. */
+void rtg_tokenizer_byte_encoder(uint32_t out[256]);
+/* Releases a buffer returned by rtg_tokenizer_encode / _decode / _pre_tokenize. */
+void rtg_free_buffer(void* p);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,6 +89,22 @@ SIGNATURES = {
     "rtg_forward_cached_batched": (Result, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "rtg_generate_cached_batched": (Result, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t,
                                              C.c_void_p, C.POINTER(Timing)]),
+    "rtg_tokenizer_from_files": (Result, [C.c_char_p, C.c_char_p, C.POINTER(C.c_void_p)]),
+    "rtg_tokenizer_from_strings": (Result, [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t, C.POINTER(C.c_void_p)]),
+    "rtg_tokenizer_from_vocab_and_merges": (Result, [C.POINTER(C.c_char_p), C.c_size_t, C.POINTER(C.c_char_p),
+                                                     C.POINTER(C.c_char_p), C.c_size_t, C.POINTER(C.c_void_p)]),
+    "rtg_tokenizer_destroy": (None, [C.c_void_p]),
+    "rtg_tokenizer_encode": (Result, [C.c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.POINTER(C.c_uint32)),
+                                      C.POINTER(C.c_size_t)]),
+    "rtg_tokenizer_decode": (Result, [C.c_void_p, C.POINTER(C.c_uint32), C.c_size_t, C.POINTER(C.c_void_p),
+                                      C.POINTER(C.c_size_t)]),
+    "rtg_tokenizer_vocab_size": (C.c_size_t, [C.c_void_p]),
+    "rtg_tokenizer_token_to_id": (C.c_bool, [C.c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_uint32)]),
+    "rtg_tokenizer_id_to_token": (C.c_bool, [C.c_void_p, C.c_uint32, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
+    "rtg_tokenizer_pre_tokenize": (Result, [C.c_char_p, C.c_size_t, C.POINTER(C.POINTER(C.c_size_t)),
+                                            C.POINTER(C.c_size_t)]),
+    "rtg_tokenizer_byte_encoder": (None, [C.POINTER(C.c_uint32)]),
+    "rtg_free_buffer": (None, [C.c_void_p]),
 }
 
 _lib = None
