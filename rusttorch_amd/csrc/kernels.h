@@ -74,6 +74,21 @@ void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past
                          int n_head, int n_pos, int d, float* out);
 
 // bf16 conversion / transposition used once at model load.
+// Token choice of one decode step on the device (sampling.hip).
+struct SampleParams {
+  float temperature;  // <= 0: greedy (argmax after the repetition penalty)
+  int top_k;          // 0 or >= V: off
+  float top_p;        // outside (0, 1): off
+  float penalty;      // 1: off
+  uint64_t seed;      // SplitMix64 seed; the draw of generation index g is number draw0 + g + 1
+  uint32_t draw0;
+};
+// Picks the token of generation index g = *step_dev - 1 from logits[V] (the
+// history is prompt[0, n_prompt) then ids[0, g)) and writes it to *token and
+// ids[g]; work[V] is scratch. False when V is too large (> 65536).
+bool launch_sample(hipStream_t s, const float* logits, int V, float* work, const uint32_t* prompt, int n_prompt,
+                   uint32_t* ids, const int* step_dev, const SampleParams& sp, uint32_t* token);
+
 // Element types of a source tensor as uploaded from the caller or the file.
 enum { SRC_F32 = 0, SRC_BF16 = 1, SRC_F16 = 2 };
 void launch_transpose_to(hipStream_t s, const void* src, int stype, int rows, int cols, void* dst, int wtype);

@@ -119,6 +119,7 @@ struct rtg_cache {
   uint32_t* ids_dev = nullptr;   // [B][P] generated ids
   uint32_t* ids_in = nullptr;    // [B*P] prompt ids
   float* att_work = nullptr;     // per-split partials of decode attention
+  float* sample_work = nullptr;  // [V] working copy of the logits for the device sampler
   // work buffers, capacity in rows
   size_t rows_cap = 0;
   float *x = nullptr, *ln = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
@@ -364,9 +365,11 @@ struct PoolLease {
   }
 };
 
-// Greedy generate_cached over B equal-length prompts (gpt2.rs:405-441).
+// generate_cached over B equal-length prompts (gpt2.rs:405-441), greedy or,
+// with sp (B = 1), choosing every token with the device sampler
+// (sample_logits, gpt2.rs:871-906): the whole loop stays on the device.
 static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t B, size_t n, size_t max_new,
-                            uint32_t* out, rtg_timing* timing) {
+                            uint32_t* out, rtg_timing* timing, const SampleParams* sp = nullptr) {
   PoolLease lease(m, B);
   rtg_cache* c = lease.c;
   const size_t V = m->cfg.vocab_size, P = m->cfg.n_positions;
@@ -374,6 +377,13 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   ensure_rows(c, B * n);
   ensure_logits(c, B * n);
   hipStream_t s = c->stream;
+  if (sp && !c->sample_work) HIPX(hipMalloc(&c->sample_work, V * 4));
+  // overwrite the argmax token of the step just enqueued with the sampler's choice
+  auto sample = [&](const float* row) {
+    if (sp && !launch_sample(s, row, (int)V, c->sample_work, c->ids_in, (int)n, c->ids_dev, c->step_dev, *sp,
+                             c->token_dev))
+      throw HipError{"vocabulary too large for the device sampler"};
+  };
   if (!c->pstate && persistent_supported(m->pplan, (int)B)) {
     c->pstate = persistent_state_create(m->pplan, c->k, c->v, (int)B, c->token_dev, c->pos_dev, c->logits, c->keys,
                                         c->ids_dev, c->step_dev);
@@ -388,15 +398,22 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   // prefill token that the first decode step consumes.
   set_counters(c, (int)n - 1, 0);
   launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev);
+  sample(c->logits + (n - 1) * V);
   HIPX(hipEventRecord(c->ev[1], s));
   // RTG_NO_GRAPH=1: enqueue each step's kernels directly instead of replaying
   // the captured step graph (for per-kernel profiling; same results).
   const char* ng = getenv("RTG_NO_GRAPH");
   if (ng && ng[0] == '1') {
-    for (size_t i = 1; i < steps; ++i) enqueue_decode_step(c);
+    for (size_t i = 1; i < steps; ++i) {
+      enqueue_decode_step(c);
+      sample(c->logits);
+    }
   } else {
     ensure_graph(c);
-    for (size_t i = 1; i < steps; ++i) HIPX(hipGraphLaunch(c->graph_exec, s));
+    for (size_t i = 1; i < steps; ++i) {
+      HIPX(hipGraphLaunch(c->graph_exec, s));
+      sample(c->logits);
+    }
   }
   HIPX(hipEventRecord(c->ev[2], s));
   // Optional profiling pass: rewind to the first decode step and replay the
@@ -404,7 +421,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   // (tokens, positions, cache rows) are the same, so are the results.
   double kern_ms = 0.0;
   size_t kern_n = 0;
-  if (timing && timing->profile_kernels && c->pstate && steps > 1) {
+  if (timing && timing->profile_kernels && c->pstate && steps > 1 && !sp) {
     std::vector<hipEvent_t> evs(2 * (steps - 1));
     for (auto& e : evs) HIPX(hipEventCreate(&e));
     set_counters(c, (int)n, 1);
@@ -860,7 +877,8 @@ void rtg_cache_destroy(rtg_cache* c) {
   if (c->pstate) persistent_state_destroy(c->pstate);
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
-                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits})
+                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits,
+                  (void*)c->sample_work})
     if (p) hipFree(p);
   for (auto e : c->ev)
     if (e) hipEventDestroy(e);
@@ -943,26 +961,16 @@ rtg_result rtg_generate_cached(const rtg_model* model, const uint32_t* prompt, s
                                float temperature, uint64_t seed, uint32_t* out) {
   if (temperature <= 0.0f) return rtg_generate_cached_batched(model, prompt, 1, n, max_new, out, nullptr);
   if (!model || !out) return err("null argument");
-  // Sampling path (gpt2.rs:405-441 with sample_with_temperature).
+  // Sampling path (gpt2.rs:405-441 with sample_with_temperature, :996-1017),
+  // tokens chosen on the device.
   std::string e = check_cached(model, 0, prompt, n);
   if (!e.empty()) return err(e);
-  const size_t V = model->cfg.vocab_size, P = model->cfg.n_positions;
+  const size_t P = model->cfg.n_positions;
   const size_t steps = max_new > 0 ? max_new : 1;
   if (n + steps - 1 > P) return err(fmt("Total sequence length %zu exceeds max position %zu", P + 1, P));
-  SplitMix rng{seed};
+  const SampleParams sp{temperature, 0, 1.0f, 1.0f, seed, 0};
   try {
-    PoolLease lease(model, 1);
-    rtg_cache* c = lease.c;
-    std::vector<float> logits(n * V);
-    forward_cached_impl(c, prompt, n, logits.data());
-    std::vector<uint32_t> toks(prompt, prompt + n);
-    toks.push_back(sample_temperature(logits.data() + (n - 1) * V, V, temperature, rng));
-    for (size_t i = 1; i < steps; ++i) {
-      uint32_t last = toks.back();
-      forward_cached_impl(c, &last, 1, logits.data());
-      toks.push_back(sample_temperature(logits.data(), V, temperature, rng));
-    }
-    memcpy(out, toks.data(), toks.size() * 4);
+    generate_greedy(model, prompt, 1, n, max_new, out, nullptr, &sp);
   } catch (const HipError& he) {
     return err(he.msg);
   }
@@ -976,23 +984,14 @@ rtg_result rtg_generate_with_config(const rtg_model* model, const uint32_t* prom
     return rtg_generate_cached_batched(model, prompt, 1, n, cfg->max_new_tokens, out, nullptr);
   std::string e = check_cached(model, 0, prompt, n);
   if (!e.empty()) return err(e);
-  const size_t V = model->cfg.vocab_size, P = model->cfg.n_positions;
+  const size_t P = model->cfg.n_positions;
   const size_t steps = cfg->max_new_tokens > 0 ? cfg->max_new_tokens : 1;
   if (n + steps - 1 > P) return err(fmt("Total sequence length %zu exceeds max position %zu", P + 1, P));
-  SplitMix rng{cfg->seed};
+  // sample_logits (gpt2.rs:871-906) on the device after every step
+  const int k = cfg->top_k > (size_t)INT32_MAX ? INT32_MAX : (int)cfg->top_k;
+  const SampleParams sp{cfg->temperature, k, cfg->top_p, cfg->repetition_penalty, cfg->seed, 0};
   try {
-    PoolLease lease(model, 1);
-    rtg_cache* c = lease.c;
-    std::vector<float> logits(n * V);
-    forward_cached_impl(c, prompt, n, logits.data());
-    std::vector<uint32_t> toks(prompt, prompt + n);
-    toks.push_back(sample_logits(logits.data() + (n - 1) * V, V, toks, *cfg, rng));
-    for (size_t i = 1; i < steps; ++i) {
-      uint32_t last = toks.back();
-      forward_cached_impl(c, &last, 1, logits.data());
-      toks.push_back(sample_logits(logits.data(), V, toks, *cfg, rng));
-    }
-    memcpy(out, toks.data(), toks.size() * 4);
+    generate_greedy(model, prompt, 1, n, cfg->max_new_tokens, out, nullptr, &sp);
   } catch (const HipError& he) {
     return err(he.msg);
   }
