@@ -85,9 +85,9 @@ struct SampleParams {
 };
 // Picks the token of generation index g = *step_dev - 1 from logits[V] (the
 // history is prompt[0, n_prompt) then ids[0, g)) and writes it to *token and
-// ids[g]; work[V] is scratch. False when V is too large (> 65536).
-bool launch_sample(hipStream_t s, const float* logits, int V, float* work, const uint32_t* prompt, int n_prompt,
-                   uint32_t* ids, const int* step_dev, const SampleParams& sp, uint32_t* token);
+// ids[g]. One workgroup, no scratch memory. False when V is too large (> 65536).
+bool launch_sample(hipStream_t s, const float* logits, int V, const uint32_t* prompt, int n_prompt, uint32_t* ids,
+                   const int* step_dev, const SampleParams& sp, uint32_t* token);
 
 // Element types of a source tensor as uploaded from the caller or the file.
 enum { SRC_F32 = 0, SRC_BF16 = 1, SRC_F16 = 2 };

@@ -119,7 +119,6 @@ struct rtg_cache {
   uint32_t* ids_dev = nullptr;   // [B][P] generated ids
   uint32_t* ids_in = nullptr;    // [B*P] prompt ids
   float* att_work = nullptr;     // per-split partials of decode attention
-  float* sample_work = nullptr;  // [V] working copy of the logits for the device sampler
   // work buffers, capacity in rows
   size_t rows_cap = 0;
   float *x = nullptr, *ln = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
@@ -377,11 +376,9 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   ensure_rows(c, B * n);
   ensure_logits(c, B * n);
   hipStream_t s = c->stream;
-  if (sp && !c->sample_work) HIPX(hipMalloc(&c->sample_work, V * 4));
   // overwrite the argmax token of the step just enqueued with the sampler's choice
   auto sample = [&](const float* row) {
-    if (sp && !launch_sample(s, row, (int)V, c->sample_work, c->ids_in, (int)n, c->ids_dev, c->step_dev, *sp,
-                             c->token_dev))
+    if (sp && !launch_sample(s, row, (int)V, c->ids_in, (int)n, c->ids_dev, c->step_dev, *sp, c->token_dev))
       throw HipError{"vocabulary too large for the device sampler"};
   };
   if (!c->pstate && persistent_supported(m->pplan, (int)B)) {
@@ -877,8 +874,7 @@ void rtg_cache_destroy(rtg_cache* c) {
   if (c->pstate) persistent_state_destroy(c->pstate);
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
-                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits,
-                  (void*)c->sample_work})
+                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits})
     if (p) hipFree(p);
   for (auto e : c->ev)
     if (e) hipEventDestroy(e);

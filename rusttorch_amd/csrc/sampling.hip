@@ -7,9 +7,22 @@
 // One workgroup of 512 threads per sequence. Element i is held in a register
 // of thread i % 512 (row i / 512: the row index is the register index, so
 // the load is one coalesced sweep and every later pass works on registers).
-// Questions in index order (the sampling CDF, the order of top-p ties) are
-// answered from per-(row, wave) partial sums kept in LDS. The repetition
-// penalty edits a copy of the logits in device memory before the load.
+// The work is VALU-bound on the one CU, so every pass over the row is kept to
+// a few instructions per element:
+//  - the repetition penalty marks the history in an LDS bitmap and counts it
+//    in an LDS hash table; each element tests its bit and, when set, applies
+//    the penalty once per occurrence to its register;
+//  - top-k and top-p find their cut-off by histogram rounds (radix select).
+//    The first round of top-k bins the scaled logits linearly (2048 bins)
+//    between their minimum and maximum, the first round of top-p bins the exponent and two
+//    mantissa bits of exp(y - max): both spread the values over many bins, so
+//    the LDS atomics rarely collide, and both maps are monotone, so the bin of
+//    the k-th value (of the mass crossing p) is exact. Later rounds refine the
+//    key bits of that bin's members only;
+//  - questions in index order (the sampling CDF, the order of top-p ties) are
+//    answered from per-(row, wave) partial sums, reduced across the wave by a
+//    transposing butterfly (one shuffle per row and stage, halving the rows at
+//    each stage).
 //
 // The uniform draw of generation index g is output number draw0 + g + 1 of
 // SplitMix64 seeded with the caller's seed, mix(seed + k * 0x9E3779B97F4A7C15),
@@ -18,8 +31,9 @@
 //
 // Sums (softmax denominators, top-p masses, the CDF) are formed in a fixed
 // order, so results are deterministic, but not in the reference's sequential
-// order: a draw within rounding distance of a CDF boundary can pick the
-// neighbouring token.
+// order, and the CDF is compared in unnormalised form (draw * total against
+// running sums of exp(y - max)): a draw within rounding distance of a CDF
+// boundary can pick the neighbouring token.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -31,42 +45,44 @@ namespace {
 constexpr int ST = 512;        // threads (2 waves per SIMD: up to 256 registers each)
 constexpr int SW = ST / 64;    // waves
 constexpr int MAX_ROWS = 128;  // V <= 65536
+constexpr int NB = 2048;       // histogram bins of the widest round (11 bits)
+constexpr int PBW = MAX_ROWS * ST / 32;  // words of the token bitmap
+constexpr int DMAX = 2048;  // distinct penalised tokens per penalty round
+constexpr uint32_t NONE = 0xffffffffu;
 
-__device__ __forceinline__ float wave_sum_s(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 __device__ __forceinline__ float wave_max_s(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+__device__ __forceinline__ float wave_min_s(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+  return v;
+}
 
 struct SampleSmem {
-  float red[SW];
-  float seg[MAX_ROWS * SW];      // per (row, wave) values, index order
-  float segpre[MAX_ROWS * SW];   // their exclusive prefix sums
-  unsigned hist[256];
-  unsigned mass[256];  // fixed-point probability mass per digit
-  unsigned long long key;
-  uint32_t hist_tokens[ST];
+  float red[2 * SW];
+  unsigned wtot[SW];
+  union {
+    struct {                        // selection and the draw
+      unsigned hist[NB];            // counts or fixed-point probability masses per bin
+      float seg[MAX_ROWS * SW];     // per (row, wave) values, index order
+      float segpre[MAX_ROWS * SW];  // their exclusive prefix sums
+    };
+    struct {                  // repetition penalty
+      uint32_t wordpre[PBW];  // marked tokens in the bitmap words before each word
+      uint32_t cnt[DMAX];     // occurrences per marked token, by rank
+      float val[DMAX];        // penalised logit per marked token, by rank
+    };
+  };
+  uint32_t pbits[PBW];  // tokens of the history (within the round's range)
   unsigned misc[8];
-  unsigned long long lmisc[2];
+  unsigned long long key;
   float fmisc[2];
 };
 
-// Sum / max over the block in a fixed order; every thread gets the result.
-__device__ float block_sum(float v, SampleSmem& sm) {
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  v = wave_sum_s(v);
-  __syncthreads();
-  if (l == 0) sm.red[w] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < SW; ++i) t += sm.red[i];
-  return t;
-}
+// Max / min over the block in a fixed order; every thread gets the result.
 __device__ float block_max(float v, SampleSmem& sm) {
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   v = wave_max_s(v);
@@ -76,6 +92,29 @@ __device__ float block_max(float v, SampleSmem& sm) {
   float t = -INFINITY;
   for (int i = 0; i < SW; ++i) t = fmaxf(t, sm.red[i]);
   return t;
+}
+__device__ void block_minmax(float& mx, float& mn, SampleSmem& sm) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  mx = wave_max_s(mx);
+  mn = wave_min_s(mn);
+  __syncthreads();
+  if (l == 0) {
+    sm.red[w] = mx;
+    sm.red[SW + w] = mn;
+  }
+  __syncthreads();
+  mx = -INFINITY;
+  mn = INFINITY;
+  for (int i = 0; i < SW; ++i) {
+    mx = fmaxf(mx, sm.red[i]);
+    mn = fminf(mn, sm.red[SW + i]);
+  }
+}
+
+// Bin of y among NB linear bins from mn (scale bs = (NB - 1) / range, or 0):
+// monotone in y; -inf and NaN go to bin 0.
+__device__ __forceinline__ unsigned lin_bin(float y, float mn, float bs) {
+  return (unsigned)fminf(fmaxf((y - mn) * bs, 0.f), (float)(NB - 1));
 }
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -98,44 +137,86 @@ __device__ __forceinline__ int lanes_before(unsigned long long ballot) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(ballot >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ballot, 0u));
 }
 
-// Wave 0 only: the largest bin b (of 256, counts or fixed-point masses h)
-// whose running total from the top, sum_{b' >= b} h[b'], reaches need, and the
-// total of the bins above it. Returns -1 when the bins do not reach need.
-template <typename T>
-__device__ int wave_top_bin(const T* h, T need, int lane, T* above_out) {
-  T v[4], s = 0;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {  // lane l: bins 255 - 4l - k, descending
-    v[k] = h[255 - 4 * lane - k];
-    s += v[k];
-  }
-  T incl = s;
+// Exclusive prefix of x over the block in thread order; the total in *total.
+__device__ unsigned block_excl_scan(unsigned x, SampleSmem& sm, unsigned* total) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  unsigned incl = x;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const T u = __shfl_up(incl, o, 64);
+    const unsigned u = __shfl_up(incl, o, 64);
     if (lane >= o) incl += u;
   }
-  T cum = incl - s;
-  int found = -1;
-  T above = 0;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    if (found < 0 && cum + v[k] >= need) {
-      found = 255 - 4 * lane - k;
-      above = cum;
-    }
-    cum += v[k];
+  __syncthreads();
+  if (lane == 63) sm.wtot[w] = incl;
+  __syncthreads();
+  unsigned base = 0, tot = 0;
+  for (int i = 0; i < SW; ++i) {
+    if (i == w) base = tot;
+    tot += sm.wtot[i];
   }
-  const unsigned long long bal = __ballot(found >= 0);
-  if (!bal) return -1;
-  const int src = __builtin_ctzll(bal);
-  *above_out = __shfl(above, src, 64);
-  return __shfl(found, src, 64);
+  *total = tot;
+  return base + incl - x;
+}
+
+// Whole block, after the histogram h[NBINS] is complete: the largest bin b
+// whose running total from the top, sum_{b' >= b} h[b'], reaches need (>= 1).
+// Leaves b (NONE when the bins do not reach need), the total of the bins above
+// it and h[b] in misc[0..2]; ends synchronised.
+template <int NBINS>
+__device__ void block_top_bin(const unsigned* h, unsigned need, SampleSmem& sm) {
+  constexpr int BPT = NBINS / ST;
+  static_assert(BPT * ST == NBINS, "bins per thread");
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  unsigned v[BPT], s = 0;
+#pragma unroll
+  for (int k = 0; k < BPT; ++k) {  // thread t: bins NBINS-1-BPT*t-k, descending
+    v[k] = h[NBINS - 1 - BPT * t - k];
+    s += v[k];
+  }
+  unsigned incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) sm.wtot[w] = incl;
+  if (t == 0) sm.misc[0] = NONE;
+  __syncthreads();
+  unsigned cum = incl - s;
+  for (int i = 0; i < w; ++i) cum += sm.wtot[i];
+  // running totals only grow: exactly one thread sees need crossed in its bins
+  if (cum < need && need <= cum + s) {
+#pragma unroll
+    for (int k = 0; k < BPT; ++k) {
+      if (cum < need && need <= cum + v[k]) {
+        sm.misc[0] = (unsigned)(NBINS - 1 - BPT * t - k);
+        sm.misc[1] = cum;
+        sm.misc[2] = v[k];
+      }
+      cum += v[k];
+    }
+  }
+  __syncthreads();
+}
+
+// A histogram round: hist_begin clears NBINS bins; the caller accumulates;
+// hist_end finds the top bin reaching need (results in misc[0..2] for every
+// thread).
+template <int NBINS>
+__device__ __forceinline__ void hist_begin(SampleSmem& sm) {
+  for (int b = threadIdx.x; b < NBINS; b += ST) sm.hist[b] = 0u;
+  __syncthreads();
+}
+template <int NBINS>
+__device__ __forceinline__ void hist_end(SampleSmem& sm, unsigned need) {
+  __syncthreads();
+  block_top_bin<NBINS>(sm.hist, need, sm);
 }
 
 // Wave 0 only: segpre[i] = sum of seg[0, i) for i < n (n <= 64 * 16), each
-// lane summing a contiguous run in order, then the runs' prefix.
-__device__ void wave_excl_prefix(const float* seg, float* segpre, int n, int lane) {
+// lane summing a contiguous run in order, then the runs' prefix. Returns the
+// total to every lane.
+__device__ float wave_excl_prefix(const float* seg, float* segpre, int n, int lane) {
   const int per = (n + 63) / 64, b = lane * per, e = min(n, b + per);
   float s = 0.f;
   for (int i = b; i < e; ++i) s += seg[i];
@@ -150,16 +231,138 @@ __device__ void wave_excl_prefix(const float* seg, float* segpre, int n, int lan
     segpre[i] = run;
     run += seg[i];
   }
+  return __shfl(incl, 63, 64);
+}
+
+// One stage of the transposing butterfly over 16-row chunks: N values per
+// lane become N/2; the lane with bit O set keeps the upper half.
+template <int N, int O>
+__device__ __forceinline__ void tr_stage(float (&a)[16], int lane) {
+  constexpr int H = N / 2;
+  const bool up = (lane & O) != 0;
+#pragma unroll
+  for (int k = 0; k < H; ++k) {
+    const float send = up ? a[k] : a[k + H];
+    const float keep = up ? a[k + H] : a[k];
+    a[k] = keep + __shfl_xor(send, O, 64);
+  }
+}
+
+// seg[row * SW + w] = sum of the wave's 64 values of each row (the 64
+// consecutive indices row * ST + w * 64 ...). After the four halving stages
+// lane l holds row (l >> 2) of its 16-row chunk, summed over its lane group;
+// two butterflies finish the sum.
+template <int NJ>
+__device__ __forceinline__ void seg_sums(const float (&v)[NJ], float* seg, int w, int lane) {
+#pragma unroll
+  for (int c0 = 0; c0 < NJ; c0 += 16) {
+    float a[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a[k] = c0 + k < NJ ? v[c0 + k] : 0.f;
+    tr_stage<16, 32>(a, lane);
+    tr_stage<8, 16>(a, lane);
+    tr_stage<4, 8>(a, lane);
+    tr_stage<2, 4>(a, lane);
+    a[0] += __shfl_xor(a[0], 2, 64);
+    a[0] += __shfl_xor(a[0], 1, 64);
+    const int r = c0 + (lane >> 2);
+    if ((lane & 3) == 0 && r < NJ) seg[r * SW + w] = a[0];
+  }
+}
+
+// Segment sums of v and their prefix (seg, segpre); returns the total.
+template <int NJ>
+__device__ __forceinline__ float seg_total(const float (&v)[NJ], SampleSmem& sm, int w, int lane) {
+  seg_sums<NJ>(v, sm.seg, w, lane);
+  __syncthreads();
+  if (w == 0) {
+    const float tot = wave_excl_prefix(sm.seg, sm.segpre, NJ * SW, lane);
+    if (lane == 0) sm.fmisc[1] = tot;
+  }
+  __syncthreads();
+  return sm.fmisc[1];
 }
 
 __device__ __forceinline__ uint32_t hist_at(const uint32_t* prompt, int n_prompt, const uint32_t* ids, int q) {
   return q < n_prompt ? prompt[q] : ids[q - n_prompt];
 }
 
+// Dense rank of a marked token: marked tokens below it.
+__device__ __forceinline__ unsigned mark_rank(const SampleSmem& sm, uint32_t tok) {
+  return sm.wordpre[tok >> 5] + (unsigned)__popc(sm.pbits[tok >> 5] & ((1u << (tok & 31u)) - 1u));
+}
+
+// gpt2.rs:909-921: for every token of the history (prompt and generated),
+// logit /= penalty if it is positive, else logit *= penalty, once per
+// occurrence. Per round of token ids (all of them at once while the history
+// has at most DMAX entries): the history's tokens are marked in an LDS bitmap,
+// the marks ranked densely (prefix popcounts of the words) and counted per
+// rank; one thread per marked token applies its occurrences to the logit as
+// loaded, and every element reads its result by rank.
+template <int NJ>
+__device__ __forceinline__ void apply_penalty(float (&v)[NJ], const float* logits, int V, const uint32_t* prompt,
+                                              int n_prompt, const uint32_t* ids, int nh, float pen, SampleSmem& sm) {
+  const int t = threadIdx.x;
+  const int span = nh <= DMAX ? V : DMAX;  // token ids per round: at most DMAX marks
+  constexpr int WPT = PBW / ST;            // bitmap words per thread in the scan
+  for (int lo = 0; lo < V; lo += span) {
+    const uint32_t hi = (uint32_t)min(V, lo + span);
+    for (int i = t; i < PBW; i += ST) sm.pbits[i] = 0u;
+    for (int i = t; i < DMAX; i += ST) sm.cnt[i] = 0u;
+    __syncthreads();
+    for (int q = t; q < nh; q += ST) {
+      const uint32_t tok = hist_at(prompt, n_prompt, ids, q);
+      if (tok >= (uint32_t)lo && tok < hi) atomicOr(&sm.pbits[tok >> 5], 1u << (tok & 31u));
+    }
+    __syncthreads();
+    unsigned pc[WPT], s = 0, marks;
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+      pc[k] = (unsigned)__popc(sm.pbits[t * WPT + k]);
+      s += pc[k];
+    }
+    unsigned run = block_excl_scan(s, sm, &marks);
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+      sm.wordpre[t * WPT + k] = run;
+      run += pc[k];
+    }
+    __syncthreads();
+    for (int q = t; q < nh; q += ST) {
+      const uint32_t tok = hist_at(prompt, n_prompt, ids, q);
+      if (tok >= (uint32_t)lo && tok < hi) atomicAdd(&sm.cnt[mark_rank(sm, tok)], 1u);
+    }
+    __syncthreads();
+    for (unsigned r = t; r < marks; r += ST) {
+      int a = 0, b = PBW - 1;  // the last word with wordpre <= r holds mark r
+      while (a < b) {
+        const int m = (a + b + 1) >> 1;
+        if (sm.wordpre[m] <= r) a = m;
+        else b = m - 1;
+      }
+      uint32_t word = sm.pbits[a];
+      for (unsigned z = r - sm.wordpre[a]; z > 0; --z) word &= word - 1u;  // drop the lower marks
+      float x = logits[a * 32 + __builtin_ctz(word)];
+      for (unsigned z = sm.cnt[r]; z > 0; --z) x = x > 0.0f ? x / pen : x * pen;
+      sm.val[r] = x;
+    }
+    __syncthreads();
+    // element j * ST + t is bit t % 32 of word j * ST / 32 + t / 32
+    const uint32_t below = (1u << (t & 31)) - 1u;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int wi = j * (ST / 32) + (t >> 5);
+      const uint32_t word = sm.pbits[wi];
+      if ((word >> (t & 31)) & 1u) v[j] = sm.val[sm.wordpre[wi] + (unsigned)__popc(word & below)];
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 
 template <int NJ>
-__global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ logits, int V, float* __restrict__ work,
+__global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ logits, int V,
                                                     const uint32_t* __restrict__ prompt, int n_prompt,
                                                     uint32_t* __restrict__ ids, const int* __restrict__ step_dev,
                                                     SampleParams sp, uint32_t* __restrict__ token) {
@@ -168,41 +371,12 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
   const int g = *step_dev - 1;  // generation index of the token being chosen
   // v[j] = element j * ST + t ("row" j), in registers for all passes
   float v[NJ];
-  const float* src = logits;
-  // ---- repetition penalty over prompt + generated tokens (gpt2.rs:909-921):
-  // once per occurrence; the first occurrence of a token in the history
-  // applies all of its occurrences, one after the other, to a copy in memory ----
-  if (sp.penalty != 1.0f) {
-    for (int i = t; i < V; i += ST) work[i] = logits[i];
-    const int nh = n_prompt + g;
-    for (int base = 0; base < nh; base += ST) {
-      __syncthreads();
-      if (base + t < nh) sm.hist_tokens[t] = hist_at(prompt, n_prompt, ids, base + t);
-      __syncthreads();
-      const int cnt = min(ST, nh - base);
-      if (t < cnt) {
-        const uint32_t tok = sm.hist_tokens[t];
-        bool first = true;
-        for (int q = 0; q < base && first; ++q) first = hist_at(prompt, n_prompt, ids, q) != tok;
-        for (int q = 0; q < t && first; ++q) first = sm.hist_tokens[q] != tok;
-        if (first && tok < (uint32_t)V) {
-          int c = 1;
-          for (int q = t + 1; q < cnt; ++q) c += sm.hist_tokens[q] == tok;
-          for (int q = base + ST; q < nh; ++q) c += hist_at(prompt, n_prompt, ids, q) == tok;
-          float x = work[tok];
-          for (int k = 0; k < c; ++k) x = x > 0.0f ? x / sp.penalty : x * sp.penalty;
-          work[tok] = x;
-        }
-      }
-    }
-    __syncthreads();
-    src = work;
-  }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int i = j * ST + t;
-    v[j] = i < V ? src[i] : -INFINITY;
+    v[j] = i < V ? logits[i] : -INFINITY;
   }
+  if (sp.penalty != 1.0f) apply_penalty<NJ>(v, logits, V, prompt, n_prompt, ids, n_prompt + g, sp.penalty, sm);
   uint32_t pick = 0;
   if (sp.temperature <= 0.0f) {
     // ---- greedy: argmax_f32 (gpt2.rs:858-868), strict '>' from -inf, the
@@ -224,159 +398,169 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
   } else {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) v[j] = v[j] / sp.temperature;
-    // ---- top-k (gpt2.rs:924-935): threshold = k-th largest value, found
-    // exactly by an 8-bit radix select on order-preserving keys ----
+    float mx;
     if (sp.top_k > 0 && sp.top_k < V) {
-      uint32_t prefix = 0, need = (uint32_t)sp.top_k;
-      for (int shift = 24; shift >= 0; shift -= 8) {
-        const uint32_t hi_mask = shift == 24 ? 0u : ~((1u << (shift + 8)) - 1u);
-        if (t < 256) sm.hist[t] = 0;
-        __syncthreads();
+      // ---- top-k (gpt2.rs:924-935): threshold = the k-th largest value ----
+      float mn = INFINITY;
+      mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
+      for (int j = 0; j < NJ; ++j)
+        if (v[j] > -INFINITY) {
+          mx = fmaxf(mx, v[j]);
+          mn = fminf(mn, v[j]);
+        }
+      block_minmax(mx, mn, sm);
+      // round 1: NB linear bins over [mn, mx]; a monotone map, so equal
+      // values share a bin and every value in a higher bin is larger
+      const float range = mx - mn;
+      const float bs = (range > 0.f && range < INFINITY) ? (float)(NB - 1) / range : 0.f;
+      hist_begin<NB>(sm);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (j * ST + t < V) atomicAdd(&sm.hist[lin_bin(v[j], mn, bs)], 1u);
+      hist_end<NB>(sm, (unsigned)sp.top_k);
+      const unsigned b1 = sm.misc[0];  // k < V elements: always found
+      unsigned need = (unsigned)sp.top_k - sm.misc[1];
+      uint32_t mm[(NJ + 31) / 32];  // members of bin b1
+#pragma unroll
+      for (int q = 0; q < (NJ + 31) / 32; ++q) mm[q] = 0u;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (j * ST + t < V && lin_bin(v[j], mn, bs) == b1) mm[j >> 5] |= 1u << (j & 31);
+      // rounds 2-4: the order-preserving key of the members, 11 + 11 + 10 bits
+      hist_begin<2048>(sm);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if ((mm[j >> 5] >> (j & 31)) & 1u) atomicAdd(&sm.hist[order_key(v[j]) >> 21], 1u);
+      hist_end<2048>(sm, need);
+      uint32_t prefix = sm.misc[0] << 21;
+      need -= sm.misc[1];
+      hist_begin<2048>(sm);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if ((mm[j >> 5] >> (j & 31)) & 1u) {
           const uint32_t k = order_key(v[j]);
-          if (j * ST + t < V && (k & hi_mask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 255u], 1u);
+          if ((k >> 21) == (prefix >> 21)) atomicAdd(&sm.hist[(k >> 10) & 2047u], 1u);
         }
-        __syncthreads();
-        if (w == 0) {
-          unsigned above = 0;
-          const int b = wave_top_bin<unsigned>(sm.hist, need, lane, &above);
-          if (lane == 0) {
-            sm.misc[0] = (uint32_t)max(b, 0);  // need <= the count in range: b >= 0
-            sm.misc[1] = need - above;
-          }
+      hist_end<2048>(sm, need);
+      prefix |= sm.misc[0] << 10;
+      need -= sm.misc[1];
+      hist_begin<1024>(sm);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if ((mm[j >> 5] >> (j & 31)) & 1u) {
+          const uint32_t k = order_key(v[j]);
+          if ((k >> 10) == (prefix >> 10)) atomicAdd(&sm.hist[k & 1023u], 1u);
         }
-        __syncthreads();
-        prefix |= sm.misc[0] << shift;
-        need = sm.misc[1];
-        __syncthreads();
-      }
+      hist_end<1024>(sm, need);
+      prefix |= sm.misc[0];
       const float thr = from_order_key(prefix);
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
         if (v[j] < thr) v[j] = -INFINITY;
+    } else {
+      mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) mx = fmaxf(mx, v[j]);
+      mx = block_max(mx, sm);
     }
-    // From here v holds the probabilities p = exp(x - max) / sum of the
-    // filtered logits x (0 for the removed ones). Top-p keeps the largest
-    // probability, so the maximum of what it leaves is the same, and the
-    // distribution sample_from_logits draws from is p / (kept mass): top-p
-    // zeroes entries in place.
-    float mx = -INFINITY;
+    // From here v holds e = exp(y - max) of the filtered logits y (0 for the
+    // removed ones), proportional to the probabilities p = e / S. Top-p keeps
+    // the largest probability, so the maximum of what it leaves is the same,
+    // and the distribution sample_from_logits draws from is e / (kept sum):
+    // top-p zeroes entries in place.
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) mx = fmaxf(mx, v[j]);
-    mx = block_max(mx, sm);
-    float loc = 0.f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      v[j] = j * ST + t < V ? expf(v[j] - mx) : 0.f;
-      loc += v[j];
-    }
-    float sum = block_sum(loc, sm);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) v[j] = v[j] / sum;
-    sum = 1.0f;  // mass of the kept entries, as a divisor of p
+    for (int j = 0; j < NJ; ++j) v[j] = v[j] > -INFINITY ? expf(v[j] - mx) : 0.f;
+    float S = seg_total<NJ>(v, sm, w, lane);
     // ---- top-p (gpt2.rs:939-970): keep the largest probabilities, ties in
     // index order, until their running sum reaches p ----
     if (sp.top_p < 1.0f && sp.top_p > 0.0f) {
-      // radix descent (8-bit digits) over the bits of the probabilities
-      // (non-negative floats order like their bits) for the cut-off value,
-      // mass(p > cut) < top_p <= mass(p >= cut), with masses summed as
+      // radix descent over the bits of e (non-negative floats order like their
+      // bits), 10 + 11 + 10 bits, for the cut-off value with
+      // mass(e > cut) < top_p <= mass(e >= cut); masses are summed as
       // integers (p * 2^31, truncated; at most 2^-31 per entry): the same
-      // total in any order.
-      const float scale = 2147483648.0f;  // 2^31
-      const unsigned target = (unsigned)(sp.top_p * scale);
-      uint32_t prefix = 0;
-      unsigned above = 0;
-      bool all = false;
-      for (int shift = 24; shift >= 0 && !all; shift -= 8) {
-        const uint32_t hi_mask = shift == 24 ? 0u : ~((1u << (shift + 8)) - 1u);
-        if (t < 256) sm.mass[t] = 0u;
-        __syncthreads();
+      // total in any order
+      const float ms = 2147483648.0f / S;  // 2^31 / S
+      const unsigned target = max(1u, (unsigned)(sp.top_p * 2147483648.0f));
+      hist_begin<1024>(sm);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (v[j] > 0.f) atomicAdd(&sm.hist[__float_as_uint(v[j]) >> 21], (unsigned)(v[j] * ms));
+      hist_end<1024>(sm, target);
+      const uint32_t b1 = sm.misc[0];
+      if (b1 != NONE) {  // else the total stays below p: everything is kept
+        unsigned above = sm.misc[1];
+        hist_begin<2048>(sm);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const uint32_t k = __float_as_uint(v[j]);
-          if (j * ST + t < V && (k & hi_mask) == prefix) atomicAdd(&sm.mass[(k >> shift) & 255u], (unsigned)(v[j] * scale));
+          if (k != 0u && (k >> 21) == b1) atomicAdd(&sm.hist[(k >> 10) & 2047u], (unsigned)(v[j] * ms));
         }
-        __syncthreads();
-        if (w == 0) {
-          unsigned ab = 0;
-          const int bin = wave_top_bin<unsigned>(sm.mass, target - above, lane, &ab);
-          if (lane == 0) {
-            sm.misc[0] = (unsigned)bin;
-            sm.misc[1] = ab;
-          }
-        }
-        __syncthreads();
-        const int bin = (int)sm.misc[0];
-        if (bin < 0) all = true;  // the total stays below p: everything is kept
-        else {
-          prefix |= (uint32_t)bin << shift;
-          above += sm.misc[1];
-        }
-        __syncthreads();
-      }
-      if (!all) {
-        // ties at the cut-off value, in index order: the first `take` are
-        // kept, as many as the running sum needs to reach p
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const bool tie = j * ST + t < V && __float_as_uint(v[j]) == prefix;
-          const unsigned long long bal = __ballot(tie);
-          if (lane == 0) sm.seg[j * SW + w] = (float)__popcll(bal);
-        }
-        __syncthreads();
-        if (w == 0) {
-          wave_excl_prefix(sm.seg, sm.segpre, NJ * SW, lane);
-          if (lane == 0) {
-            const unsigned qcut = (unsigned)(__uint_as_float(prefix) * scale);
-            sm.misc[2] = qcut ? (target - above + qcut - 1) / qcut : 0xffffffffu;
-          }
-        }
-        __syncthreads();
-        const unsigned take = sm.misc[2];
-        loc = 0.f;
+        hist_end<2048>(sm, target - above);
+        const uint32_t p21 = (b1 << 11) | sm.misc[0];
+        above += sm.misc[1];
+        hist_begin<1024>(sm);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const uint32_t k = __float_as_uint(v[j]);
-          const bool tie = j * ST + t < V && k == prefix;
-          const unsigned long long bal = __ballot(tie);
-          bool keep = k > prefix;
-          if (tie) keep = (unsigned)sm.segpre[j * SW + w] + (unsigned)lanes_before(bal) < take;
-          if (!keep) v[j] = 0.f;
-          loc += v[j];
+          if (k != 0u && (k >> 10) == p21) atomicAdd(&sm.hist[k & 1023u], (unsigned)(v[j] * ms));
         }
-        sum = block_sum(loc, sm);
+        hist_end<1024>(sm, target - above);
+        const uint32_t cut = (p21 << 10) | sm.misc[0];
+        above += sm.misc[1];
+        const unsigned qcut = (unsigned)(__uint_as_float(cut) * ms);
+        // entries equal to the cut-off all weigh qcut; the first `take` of them
+        // in index order are kept, as many as the running sum needs to reach p
+        const unsigned take = qcut ? (target - above + qcut - 1) / qcut : 0xffffffffu;
+        const unsigned ties = qcut ? sm.misc[2] / qcut : 0xffffffffu;
+        if (qcut == 0u || ties <= take) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            if (__float_as_uint(v[j]) < cut) v[j] = 0.f;
+        } else {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const unsigned long long bal = __ballot(__float_as_uint(v[j]) == cut);
+            if (lane == 0) sm.seg[j * SW + w] = (float)__popcll(bal);
+          }
+          __syncthreads();
+          if (w == 0) wave_excl_prefix(sm.seg, sm.segpre, NJ * SW, lane);
+          __syncthreads();
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const uint32_t k = __float_as_uint(v[j]);
+            const bool tie = k == cut;
+            const unsigned long long bal = __ballot(tie);
+            bool keep = k > cut;
+            if (tie) keep = (unsigned)sm.segpre[j * SW + w] + (unsigned)lanes_before(bal) < take;
+            if (!keep) v[j] = 0.f;
+          }
+        }
+        S = seg_total<NJ>(v, sm, w, lane);
       }
     }
     // ---- sample_from_logits (gpt2.rs:973-993): the first index whose
-    // running sum of probabilities exceeds the uniform draw ----
+    // running sum of probabilities exceeds the uniform draw, here the first
+    // whose running sum of e exceeds draw * S ----
     const float r = (float)(splitmix_at(sp.seed, (uint64_t)sp.draw0 + (uint64_t)g + 1) >> 40) * (1.0f / 16777216.0f);
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      v[j] = v[j] / sum;
-      const float ws = wave_sum_s(v[j]);
-      if (lane == 0) sm.seg[j * SW + w] = ws;
-    }
-    __syncthreads();
+    const float rs = r * S;
     if (w == 0) {
-      // the (row, wave) segment of 64 indices where the running sum first exceeds r
+      // the (row, wave) segment of 64 indices where the running sum first exceeds rs
       const int n = NJ * SW;
-      wave_excl_prefix(sm.seg, sm.segpre, n, lane);
       const int per = (n + 63) / 64, b0 = lane * per, e0 = min(n, b0 + per);
       int found = -1;
       for (int i = b0; i < e0 && found < 0; ++i)
-        if (r < sm.segpre[i] + sm.seg[i]) found = i;
+        if (rs < sm.segpre[i] + sm.seg[i]) found = i;
       const unsigned long long bal = __ballot(found >= 0);
       const int segi = bal ? __shfl(found, __builtin_ctzll(bal), 64) : -1;
       if (lane == 0) {
-        sm.misc[3] = segi < 0 ? 0xffffffffu : (unsigned)segi;
+        sm.misc[3] = segi < 0 ? NONE : (unsigned)segi;
         sm.fmisc[0] = segi < 0 ? 0.f : sm.segpre[segi];
       }
     }
     __syncthreads();
     const unsigned seg = sm.misc[3];
-    if (seg == 0xffffffffu) {
+    if (seg == NONE) {
       pick = (uint32_t)(V - 1);
     } else {
       // inside the segment: 64 consecutive indices, held by wave seg % SW in row seg / SW
@@ -393,8 +577,8 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
           const float u = __shfl_up(incl, o, 64);
           if (lane >= o) incl += u;
         }
-        const unsigned long long bal = __ballot(i < V && r < sm.fmisc[0] + incl);
-        // the segment's sum (a tree) put r inside it; should the running sum
+        const unsigned long long bal = __ballot(i < V && rs < sm.fmisc[0] + incl);
+        // the segment's sum (a tree) put rs inside it; should the running sum
         // (another order) stop short by rounding, the segment's last index of
         // non-zero probability is the one the draw falls on
         const unsigned long long nz = __ballot(i < V && p > 0.f);
@@ -413,9 +597,9 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
   }
 }
 
-bool launch_sample(hipStream_t s, const float* logits, int V, float* work, const uint32_t* prompt, int n_prompt,
-                   uint32_t* ids, const int* step_dev, const SampleParams& sp, uint32_t* token) {
-#define RTG_SAMPLE(NJ) sample_kernel<NJ><<<1, ST, 0, s>>>(logits, V, work, prompt, n_prompt, ids, step_dev, sp, token)
+bool launch_sample(hipStream_t s, const float* logits, int V, const uint32_t* prompt, int n_prompt, uint32_t* ids,
+                   const int* step_dev, const SampleParams& sp, uint32_t* token) {
+#define RTG_SAMPLE(NJ) sample_kernel<NJ><<<1, ST, 0, s>>>(logits, V, prompt, n_prompt, ids, step_dev, sp, token)
   if (V <= 0) return false;
   if (V <= 1 * ST) RTG_SAMPLE(1);
   else if (V <= 4 * ST) RTG_SAMPLE(4);
