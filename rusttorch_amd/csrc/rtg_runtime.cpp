@@ -14,7 +14,6 @@
 #include <map>
 #include <memory>
 #include <mutex>
-#include <numeric>
 #include <string>
 #include <vector>
 
@@ -468,113 +467,6 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
 }
 
 // ---------------------------------------------------------------------------
-// Host-side sampling (gpt2.rs:871-1017), seeded instead of thread_rng.
-// ---------------------------------------------------------------------------
-
-namespace {
-struct SplitMix {
-  uint64_t s;
-  uint64_t next() {
-    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-  }
-  float uniform() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }  // [0, 1)
-};
-
-uint32_t argmax_host(const float* v, size_t n) {
-  size_t best = 0;
-  float bv = -INFINITY;
-  for (size_t i = 0; i < n; ++i)
-    if (v[i] > bv) {
-      bv = v[i];
-      best = i;
-    }
-  return (uint32_t)best;
-}
-
-void rep_penalty(std::vector<float>& l, const std::vector<uint32_t>& toks, float pen) {
-  for (uint32_t t : toks)
-    if (t < l.size()) l[t] = l[t] > 0.0f ? l[t] / pen : l[t] * pen;
-}
-
-void top_k(std::vector<float>& l, size_t k) {
-  std::vector<float> s(l);
-  std::stable_sort(s.begin(), s.end(), [](float a, float b) { return a > b; });
-  const float thr = s[std::min(k, s.size()) - 1];
-  for (float& v : l)
-    if (v < thr) v = -INFINITY;
-}
-
-std::vector<float> softmax_host(const std::vector<float>& l) {
-  float mx = -INFINITY;
-  for (float v : l) mx = std::fmax(mx, v);
-  std::vector<float> p(l.size());
-  float sum = 0.f;
-  for (size_t i = 0; i < l.size(); ++i) {
-    p[i] = expf(l[i] - mx);
-    sum += p[i];
-  }
-  for (float& v : p) v = v / sum;
-  return p;
-}
-
-void top_p(std::vector<float>& l, float pthr) {
-  std::vector<float> p = softmax_host(l);
-  std::vector<size_t> idx(p.size());
-  std::iota(idx.begin(), idx.end(), 0);
-  std::stable_sort(idx.begin(), idx.end(), [&](size_t a, size_t b) { return p[a] > p[b]; });
-  std::vector<char> keep(p.size(), 0);
-  float cum = 0.f;
-  for (size_t i : idx) {
-    keep[i] = 1;
-    cum += p[i];
-    if (cum >= pthr) break;
-  }
-  for (size_t i = 0; i < l.size(); ++i)
-    if (!keep[i]) l[i] = -INFINITY;
-}
-
-uint32_t sample_from(const std::vector<float>& l, SplitMix& rng) {
-  std::vector<float> p = softmax_host(l);
-  const float r = rng.uniform();
-  float cum = 0.f;
-  for (size_t i = 0; i < p.size(); ++i) {
-    cum += p[i];
-    if (r < cum) return (uint32_t)i;
-  }
-  return (uint32_t)(p.size() - 1);
-}
-
-// sample_logits, gpt2.rs:871-906.
-uint32_t sample_logits(const float* logits, size_t V, const std::vector<uint32_t>& toks, const rtg_gen_config& cfg,
-                       SplitMix& rng) {
-  if (cfg.temperature <= 0.0f) {
-    if (cfg.repetition_penalty != 1.0f) {
-      std::vector<float> mod(logits, logits + V);
-      rep_penalty(mod, toks, cfg.repetition_penalty);
-      return argmax_host(mod.data(), V);
-    }
-    return argmax_host(logits, V);
-  }
-  std::vector<float> mod(logits, logits + V);
-  if (cfg.repetition_penalty != 1.0f) rep_penalty(mod, toks, cfg.repetition_penalty);
-  for (float& v : mod) v /= cfg.temperature;
-  if (cfg.top_k > 0 && cfg.top_k < V) top_k(mod, cfg.top_k);
-  if (cfg.top_p < 1.0f && cfg.top_p > 0.0f) top_p(mod, cfg.top_p);
-  return sample_from(mod, rng);
-}
-
-// sample_with_temperature, gpt2.rs:986-1017.
-uint32_t sample_temperature(const float* logits, size_t V, float temperature, SplitMix& rng) {
-  std::vector<float> mod(logits, logits + V);
-  for (float& v : mod) v = v / temperature;
-  return sample_from(mod, rng);
-}
-}  // namespace
-
-// ---------------------------------------------------------------------------
 // Model construction (gpt2.rs:214-263)
 // ---------------------------------------------------------------------------
 
@@ -997,35 +889,56 @@ rtg_result rtg_generate_with_config(const rtg_model* model, const uint32_t* prom
 rtg_result rtg_generate(const rtg_model* model, const uint32_t* prompt, size_t n, size_t max_new, float temperature,
                         uint64_t seed, uint32_t* out) {
   if (!model || !out) return err("null argument");
-  // gpt2.rs:311-346: each step runs forward() over the last n_positions tokens.
+  // gpt2.rs:311-346: each step runs forward() over the last n_positions
+  // tokens and picks the next token from the last row's logits. The tokens
+  // live in one device buffer: the step reads its window from there and the
+  // device sampler appends its choice, so the loop never waits for the host.
   const size_t V = model->cfg.vocab_size, P = model->cfg.n_positions;
-  std::vector<uint32_t> toks(prompt, prompt + n);
-  SplitMix rng{seed};
+  if (max_new == 0) {
+    memcpy(out, prompt, n * 4);
+    return ok();
+  }
+  if (n == 0) return err("Empty input");
+  // forward() checks the ids of each window; later windows add only sampled ids
+  const size_t start0 = n > P ? n - P : 0;
+  std::string e = check_ids(model, prompt + start0, n - start0);
+  if (!e.empty()) return err(e);
+  const size_t total = n + max_new;
+  uint32_t* toks = nullptr;
+  int* steps = nullptr;
   try {
     PoolLease lease(model, 1);
     rtg_cache* c = lease.c;
+    hipStream_t s = c->stream;
+    HIPX(hipMalloc(&toks, total * 4));
+    HIPX(hipMalloc(&steps, max_new * 4));
+    std::vector<int> step_no(max_new);
+    for (size_t i = 0; i < max_new; ++i) step_no[i] = (int)(i + 1);  // the sampler's generation index + 1
+    HIPX(hipMemcpyAsync(toks, prompt, n * 4, hipMemcpyHostToDevice, s));
+    HIPX(hipMemcpyAsync(steps, step_no.data(), max_new * 4, hipMemcpyHostToDevice, s));
+    c->len = 0;
+    ensure_rows(c, std::min(total - 1, P));
+    ensure_logits(c, 1);
+    // sample_with_temperature (gpt2.rs:996-1017); argmax for temperature <= 0.
+    // Draw k of the seeded sequence goes to generation index k - 1.
+    const SampleParams sp{temperature, 0, 1.0f, 1.0f, seed, 0};
     for (size_t i = 0; i < max_new; ++i) {
-      const size_t start = toks.size() > P ? toks.size() - P : 0;
-      const size_t ctx = toks.size() - start;
-      if (ctx == 0) return err("Empty input");
-      std::string e = check_ids(model, toks.data() + start, ctx);
-      if (!e.empty()) return err(e);
-      c->len = 0;
-      ensure_rows(c, ctx);
-      ensure_logits(c, 1);
-      HIPX(hipMemcpyAsync(c->ids_in, toks.data() + start, ctx * 4, hipMemcpyHostToDevice, c->stream));
-      enqueue_prefill(c, c->ids_in, 1, ctx, 0, 1);  // logits of the last row only
-      std::vector<float> row(V);
-      HIPX(hipMemcpyAsync(row.data(), c->logits, V * 4, hipMemcpyDeviceToHost, c->stream));
-      HIPX(hipStreamSynchronize(c->stream));
-      toks.push_back(temperature <= 0.0f ? argmax_host(row.data(), V)
-                                         : sample_temperature(row.data(), V, temperature, rng));
+      const size_t len = n + i;
+      const size_t start = len > P ? len - P : 0;
+      enqueue_prefill(c, toks + start, 1, len - start, 0, 1);  // logits of the last row only
+      if (!launch_sample(s, c->logits, (int)V, toks, (int)n, toks + n, steps + i, sp, c->token_dev))
+        throw HipError{"vocabulary too large for the device sampler"};
     }
+    HIPX(hipMemcpyAsync(out, toks, total * 4, hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
     c->len = 0;
   } catch (const HipError& he) {
+    if (toks) hipFree(toks);
+    if (steps) hipFree(steps);
     return err(he.msg);
   }
-  memcpy(out, toks.data(), toks.size() * 4);
+  hipFree(toks);
+  hipFree(steps);
   return ok();
 }
 

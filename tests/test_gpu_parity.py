@@ -105,6 +105,13 @@ def test_reference_shapes_and_errors():
     with pytest.raises(Gpt2Error, match=r"^Token ID 10 out of range \(vocab_size=10\)$"):
         m.forward([1, 10])
     assert len(m.generate([0, 1], 3, 0.0)) == 5
+    with pytest.raises(Gpt2Error, match="^Empty input$"):
+        m.generate([], 2, 0.0)
+    assert m.generate([3, 4], 0, 0.0) == [3, 4]
+    with pytest.raises(Gpt2Error, match=r"^Token ID 10 out of range \(vocab_size=10\)$"):
+        m.generate([1, 10], 2, 0.0)
+    # generate checks ids through forward() of each window: one before the first window is never read
+    assert len(m.generate([10] + [1] * 16, 2, 0.0)) == 19
     assert len(m.generate_cached([0, 1, 2], 7, 0.0)) == 10
     assert len(m.generate_cached([0, 1, 2], 0, 0.0)) == 4
     assert m.num_parameters() == synth.num_parameters(sh)
@@ -255,6 +262,29 @@ def test_device_sampler_temperature_only():
             _assert_in_cdf_interval(x, got, r, g)
         if g + 1 < 16:
             logits = m.forward_cached([got], c)[0]
+
+
+@pytest.mark.parametrize("name,n_prompt,steps", [("tiny_rand", 3, 20), ("mini", 8, 12)])
+def test_uncached_generate_samples_on_device(name, n_prompt, steps):
+    """generate with temperature > 0 (gpt2.rs:311-346 with
+    sample_with_temperature, :996-1017): every step's token is chosen on the
+    device from the last row of its window's logits. Replayed through the
+    library's forward over the same windows (crossing n_positions for
+    tiny_rand) with the same seeded draws, each token is the restatement's
+    pick or within 1e-5 of the draw in the float64 CDF."""
+    from oracle import sampling_ref as S
+    _, sh, m = gpu_model(name)
+    p = synth.make_tokens(n_prompt, sh.vocab_size, stream=13).tolist()
+    ids = m.generate(p, steps, 0.9, seed=5)
+    assert len(ids) == n_prompt + steps and ids[:n_prompt] == p
+    assert ids == m.generate(p, steps, 0.9, seed=5)
+    for g in range(steps):
+        n = n_prompt + g
+        logits = m.forward(ids[max(0, n - sh.n_positions):n])[-1]
+        r = S.splitmix_uniform(5, g + 1)
+        want, _, _, x = S.choose(logits, [], 0.9, 0, 1.0, 1.0, r)
+        if ids[n] != want:
+            _assert_in_cdf_interval(x, ids[n], r, g)
 
 
 # ---------------------------------------------------------------------------
