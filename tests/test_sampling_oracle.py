@@ -76,3 +76,46 @@ def test_splitmix_and_cdf():
     x = np.log(arr(0.1, 0.2, 0.3, 0.4))
     for r, want in ((0.05, 0), (0.1, 1), (0.29, 1), (0.31, 2), (0.61, 3), (0.99, 3)):
         assert S.sample_from_logits(x, np.float32(r))[0] == want
+
+
+def test_splitmix_published_vector():
+    # the published outputs of splitmix64.c (Vigna) for seed 1234567; the
+    # uniform is their top 24 bits
+    want = [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431,
+            16408922859458223821]
+    for k, z in enumerate(want, start=1):
+        assert S.splitmix_uniform(1234567, k) == np.float32(z >> 40) / np.float32(2 ** 24)
+
+
+def test_filters_against_brute_force():
+    """top-k by counting larger entries, top-p by walking (probability desc,
+    index asc) pairs with a float32 running sum, the draw by np.searchsorted on
+    the float32 CDF: other formulations of the same rules, on random logits
+    with planted ties."""
+    rng = np.random.default_rng(5)
+    for trial in range(200):
+        n = int(rng.integers(1, 40))
+        x = rng.normal(0, 2, n).astype(np.float32)
+        if n > 3:
+            x[rng.integers(0, n, 3)] = x[0]  # ties
+        k = int(rng.integers(1, n + 1))
+        got = x.copy()
+        S.apply_top_k(got, k)
+        for i in range(n):
+            larger = int(np.sum(x > x[i]))
+            assert (got[i] == x[i]) == (larger < k) and (got[i] == -np.inf) == (larger >= k)
+        p = float(rng.uniform(0.05, 0.99))
+        got = x.copy()
+        S.apply_top_p(got, p)
+        probs = S._softmax(x)
+        kept, cum = set(), np.float32(0)
+        for _, i in sorted((-float(probs[i]), i) for i in range(n)):
+            kept.add(i)
+            cum = np.float32(cum + probs[i])
+            if cum >= np.float32(p):
+                break
+        assert {i for i in range(n) if got[i] != -np.inf} == kept
+        r = np.float32(rng.uniform(0, 1))
+        cdf = np.cumsum(S._softmax(x), dtype=np.float32)
+        want = min(int(np.searchsorted(cdf, r, side="right")), n - 1)
+        assert S.sample_from_logits(x, r)[0] == want
