@@ -95,7 +95,7 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   const int P = (int)w.cfg.n_positions;
   int dev = 0, cus = 0;
   hipGetDevice(&dev);
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus != pk::G)
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < pk::G)
     return pl;
   if (H <= 0 || d != H * pk::HD || L <= 0 || P <= 0) return pl;
   const void* fn = nullptr;
