@@ -380,6 +380,9 @@ def test_small_long_context_decode(O):
     # 650: the chunk count is capped (12 heads x 5 chunks), chunks exceed the
     # LDS stage and are streamed through it window by window
     _decode_parity(O, sd, sh, m, 650, 4, 2, stream=451)
+    # 1016 + 8: the last step attends over all n_positions = 1024 positions
+    # (the largest context the cache holds)
+    _decode_parity(O, sd, sh, m, 1016, 8, 2, stream=452)
 
 
 def test_medium_decode(O):
