@@ -47,12 +47,19 @@ def decode_bytes(sh, B, past, wbytes):
     return wb + kv + emb + B * V * 4
 
 
-def cpu_baseline(sd, sh, prompt, n_decode):
-    """Time the CPU oracle (a C restatement of gpt2.rs, 1 thread, as the
-    reference's single-threaded ndarray GEMM) on a bounded c1 sample."""
-    from oracle import oracle as O
-    O.build()
-    m = O.OracleModel.from_shape(sd, sh, threads=1)
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_oracle(m, O, prompt, n_decode):
+    """(prefill seconds, decode seconds) of one greedy run on a fresh cache."""
     c = m.new_cache()
     t0 = time.perf_counter()
     lg = m.forward_cached(prompt, c)
@@ -61,11 +68,26 @@ def cpu_baseline(sd, sh, prompt, n_decode):
     for _ in range(n_decode):
         lg = m.forward_cached([tok], c)
         tok = O.argmax(lg[0])
-    t2 = time.perf_counter()
-    return {"value": n_decode / (t2 - t1), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"c1 prompt {len(prompt)} prefill ({(t1 - t0) * 1e3:.0f} ms) then {n_decode} greedy decode "
-                      f"steps; oracle/gpt2_oracle.c (C restatement of gpt2.rs), 1 thread",
-            "prefill_tok_s": len(prompt) / (t1 - t0)}
+    return t1 - t0, time.perf_counter() - t1
+
+
+def cpu_baseline(sd, sh, prompt, n_decode, all_threads):
+    """Time the CPU oracle (a C restatement of gpt2.rs) on a bounded c1
+    sample: with 1 thread, as the reference's single-threaded ndarray GEMM
+    (the reported value), and with all_threads GEMM threads beside it."""
+    from oracle import oracle as O
+    O.build()
+    m = O.OracleModel.from_shape(sd, sh, threads=1)
+    pre, dec = _time_oracle(m, O, prompt, n_decode)
+    out = {"value": n_decode / dec, "unit": "tokens/s", "cores": 1, "kind": "port",
+           "sample": f"c1 prompt {len(prompt)} prefill ({pre * 1e3:.0f} ms) then {n_decode} greedy decode "
+                     f"steps; oracle/gpt2_oracle.c (C restatement of gpt2.rs), 1 thread",
+           "prefill_tok_s": len(prompt) / pre, "cpu": _cpu_model(), "nproc": os.cpu_count()}
+    if all_threads > 1:
+        m.set_threads(all_threads)
+        pre, dec = _time_oracle(m, O, prompt, n_decode)
+        out["all_cores"] = {"threads": all_threads, "value": n_decode / dec, "prefill_tok_s": len(prompt) / pre}
+    return out
 
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
@@ -170,6 +192,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="c1", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
     ap.add_argument("--cpu-decode-steps", type=int, default=24)
+    # a GPU box gives one GPU a 16-core CPU share, whatever os.cpu_count() says
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1),
+                    help="GEMM threads of the all-cores CPU variant (the reported value uses 1)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one device-to-device copy of 256 MiB (untimed): the reference kernel that "
@@ -253,7 +278,7 @@ def main():
     }
     if not a.no_cpu and a.workload == "c1":
         print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(sd, sh, prompts[0], a.cpu_decode_steps)
+        out["cpu_baseline"] = cpu_baseline(sd, sh, prompts[0], a.cpu_decode_steps, a.cpu_threads)
     print(json.dumps(out))
 
 
