@@ -47,14 +47,24 @@ def apply_top_k(x: np.ndarray, k: int) -> None:  # gpt2.rs:924-935
     x[x < thr] = -np.inf
 
 
-def apply_top_p(x: np.ndarray, p: float) -> None:  # gpt2.rs:939-970
-    probs = _softmax(x)
+def apply_top_p(x: np.ndarray, p: float, exact: bool = False) -> None:  # gpt2.rs:939-970
+    """exact=False: the reference's sequential f32 running sum. exact=True:
+    the same rule on float64 probabilities and sums, the cut that the
+    reference's f32 sum approximates: over thousands of kept entries its
+    drift (~1e-6) can move the cut by an entry, and which of the two a
+    summation order lands on is not fixed by the reference."""
+    if exact:
+        x64 = x.astype(np.float64)
+        probs = np.exp(x64 - np.max(x64))
+        probs /= probs.sum()
+    else:
+        probs = _softmax(x)
     order = np.argsort(-probs, kind="stable")
-    cum = np.cumsum(probs[order], dtype=np.float32)
+    cum = np.cumsum(probs[order], dtype=np.float64 if exact else np.float32)
     keep = np.zeros(x.size, dtype=bool)
     for j, i in enumerate(order):
         keep[i] = True
-        if cum[j] >= np.float32(p):
+        if cum[j] >= (p if exact else np.float32(p)):
             break
     x[~keep] = -np.inf
 
@@ -75,9 +85,11 @@ def argmax_f32(x: np.ndarray) -> int:  # gpt2.rs:858-868: strict '>' from -inf, 
     return best
 
 
-def choose(logits: np.ndarray, tokens, temperature: float, top_k: int, top_p: float, penalty: float, r):
+def choose(logits: np.ndarray, tokens, temperature: float, top_k: int, top_p: float, penalty: float, r,
+           exact_top_p: bool = False):
     """sample_logits (gpt2.rs:871-906). Returns (token, cdf_lo, cdf_hi, filtered
-    logits); for the greedy branch the cdf bounds are None."""
+    logits); for the greedy branch the cdf bounds are None. exact_top_p: the
+    float64 top-p cut (see apply_top_p)."""
     x = np.array(logits, dtype=np.float32)
     if temperature <= 0:
         if penalty != 1.0:
@@ -89,6 +101,6 @@ def choose(logits: np.ndarray, tokens, temperature: float, top_k: int, top_p: fl
     if 0 < top_k < x.size:
         apply_top_k(x, top_k)
     if 0.0 < top_p < 1.0:
-        apply_top_p(x, top_p)
+        apply_top_p(x, top_p, exact_top_p)
     i, lo, hi = sample_from_logits(x, r)
     return i, lo, hi, x

@@ -125,6 +125,12 @@ __device__ __forceinline__ float from_order_key(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+// Fixed-point probability mass of e (scale ms = 2^31 / sum): rounded to
+// nearest, so the error of a sum over many entries stays unbiased (truncation
+// would lose half a unit per entry: ~1e-5 over 45k kept entries, enough to
+// move the top-p cut).
+__device__ __forceinline__ unsigned mass_of(float e, float ms) { return (unsigned)(e * ms + 0.5f); }
+
 __device__ __forceinline__ uint64_t splitmix_at(uint64_t seed, uint64_t k) {
   uint64_t z = seed + k * 0x9E3779B97F4A7C15ull;
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -478,14 +484,14 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
       // radix descent over the bits of e (non-negative floats order like their
       // bits), 10 + 11 + 10 bits, for the cut-off value with
       // mass(e > cut) < top_p <= mass(e >= cut); masses are summed as
-      // integers (p * 2^31, truncated; at most 2^-31 per entry): the same
-      // total in any order
+      // integers (p * 2^31 rounded to nearest, mass_of): the same total in
+      // any order
       const float ms = 2147483648.0f / S;  // 2^31 / S
       const unsigned target = max(1u, (unsigned)(sp.top_p * 2147483648.0f));
       hist_begin<1024>(sm);
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
-        if (v[j] > 0.f) atomicAdd(&sm.hist[__float_as_uint(v[j]) >> 21], (unsigned)(v[j] * ms));
+        if (v[j] > 0.f) atomicAdd(&sm.hist[__float_as_uint(v[j]) >> 21], mass_of(v[j], ms));
       hist_end<1024>(sm, target);
       const uint32_t b1 = sm.misc[0];
       if (b1 != NONE) {  // else the total stays below p: everything is kept
@@ -494,7 +500,7 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const uint32_t k = __float_as_uint(v[j]);
-          if (k != 0u && (k >> 21) == b1) atomicAdd(&sm.hist[(k >> 10) & 2047u], (unsigned)(v[j] * ms));
+          if (k != 0u && (k >> 21) == b1) atomicAdd(&sm.hist[(k >> 10) & 2047u], mass_of(v[j], ms));
         }
         hist_end<2048>(sm, target - above);
         const uint32_t p21 = (b1 << 11) | sm.misc[0];
@@ -503,12 +509,12 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const uint32_t k = __float_as_uint(v[j]);
-          if (k != 0u && (k >> 10) == p21) atomicAdd(&sm.hist[k & 1023u], (unsigned)(v[j] * ms));
+          if (k != 0u && (k >> 10) == p21) atomicAdd(&sm.hist[k & 1023u], mass_of(v[j], ms));
         }
         hist_end<1024>(sm, target - above);
         const uint32_t cut = (p21 << 10) | sm.misc[0];
         above += sm.misc[1];
-        const unsigned qcut = (unsigned)(__uint_as_float(cut) * ms);
+        const unsigned qcut = mass_of(__uint_as_float(cut), ms);
         // entries equal to the cut-off all weigh qcut; the first `take` of them
         // in index order are kept, as many as the running sum needs to reach p
         const unsigned take = qcut ? (target - above + qcut - 1) / qcut : 0xffffffffu;

@@ -209,10 +209,50 @@ def test_device_sampler_matches_oracle(name, kw):
     reference's own sequential f32 CDF is off by ~1e-5, so which neighbour a
     draw lands on depends on the summation order; the greedy branch has no
     such freedom and must match exactly.)"""
-    from oracle import sampling_ref as S
     _, sh, m = gpu_model(name)
-    p = synth.make_tokens(8, sh.vocab_size, stream=11).tolist()
-    steps = 24
+    near = _sampler_replay(m, sh, kw, steps=24, stream=11)
+    if name == "mini":  # peaked distributions over 512 tokens: rounding never decides
+        assert near == 0
+
+
+@pytest.mark.parametrize("vocab", [600, 5000, 20000, 60000])
+def test_device_sampler_vocab_sizes(vocab):
+    """The sampler is built for 1, 4, 16, 64, 100 and 128 logits per thread
+    (vocabularies up to 512, 2048, 8192, 32768, 51200 and 65536); mini and
+    GPT-2 cover 1 and 100, these vocabularies the others."""
+    sh = synth.ModelShape(vocab, 64, 128, 2, 2)
+    m = Gpt2Model.from_state_dict(synth.make_weights(sh), cfg_of(sh))
+    print(f"[gpu] sampler vocab {vocab}", flush=True)
+    try:
+        for kw in (dict(temperature=0.9, top_k=50, top_p=0.95, repetition_penalty=1.2),
+                   dict(temperature=1.1, top_k=0, top_p=0.8, repetition_penalty=1.0),
+                   dict(temperature=0.0, top_k=0, top_p=1.0, repetition_penalty=1.3)):
+            _sampler_replay(m, sh, kw, steps=10, stream=20)
+    finally:
+        m.close()
+
+
+def test_device_sampler_long_history():
+    """Histories over 2048 tokens take the penalty's multi-round path (token
+    ids in rounds of 2048); a 2560-position model with a repetitive 2100-token
+    prompt reaches it, greedy with a penalty (exact) and sampled."""
+    sh = synth.ModelShape(5000, 2560, 128, 2, 2)
+    m = Gpt2Model.from_state_dict(synth.make_weights(sh), cfg_of(sh))
+    print("[gpu] sampler long history", flush=True)
+    try:
+        for kw in (dict(temperature=0.0, top_k=0, top_p=1.0, repetition_penalty=1.3),
+                   dict(temperature=0.9, top_k=50, top_p=0.95, repetition_penalty=1.2)):
+            _sampler_replay(m, sh, kw, steps=6, stream=21, n_prompt=2100, distinct=300)
+    finally:
+        m.close()
+
+
+def _sampler_replay(m, sh, kw, steps, stream, n_prompt=8, distinct=None):
+    """Runs generate_with_config and checks each token against the
+    restatement's choice from the library's teacher-forced logits; returns how
+    many tokens were decided by rounding (accepted by the CDF interval)."""
+    from oracle import sampling_ref as S
+    p = synth.make_tokens(n_prompt, distinct or sh.vocab_size, stream=stream).tolist()  # ids < distinct repeat
     cfg = GenerationConfig(max_new_tokens=steps, seed=1234 + len(kw), **kw)
     ids = m.generate_with_config(p, cfg)
     assert len(ids) == len(p) + steps and ids[:len(p)] == p
@@ -226,23 +266,35 @@ def test_device_sampler_matches_oracle(name, kw):
         got = ids[len(p) + g]
         if got != want:
             assert lo is not None, f"greedy pick {got} != {want} at step {g}"
+            if not _in_cdf_interval(x, got, r) and 0.0 < cfg.top_p < 1.0:
+                # the reference's f32 top-p sum may cut one entry away from the exact cut
+                x = S.choose(logits, toks, cfg.temperature, cfg.top_k, cfg.top_p, cfg.repetition_penalty, r,
+                             exact_top_p=True)[3]
             _assert_in_cdf_interval(x, got, r, g)
             near += 1
         toks.append(got)
         if g + 1 < steps:
             logits = m.forward_cached([got], c)[0]
-    if name == "mini":  # peaked distributions over 512 tokens: rounding never decides
-        assert near == 0
+    return near
+
+
+def _cdf_interval(x, got):
+    x64 = x.astype(np.float64)
+    p64 = np.exp(x64 - np.max(x64))
+    cum = np.cumsum(p64 / p64.sum())
+    return (cum[got - 1] if got else 0.0), cum[got], bool(np.isfinite(x64[got]))
+
+
+def _in_cdf_interval(x, got, r):
+    lo, hi, finite = _cdf_interval(x, got)
+    return finite and lo - 1e-5 <= float(r) < hi + 1e-5
 
 
 def _assert_in_cdf_interval(x, got, r, g):
     """The draw r falls in token got's interval of the float64 CDF of the
     filtered logits x, up to 1e-5."""
-    x64 = x.astype(np.float64)
-    p64 = np.exp(x64 - np.max(x64))
-    cum = np.cumsum(p64 / p64.sum())
-    lo, hi = (cum[got - 1] if got else 0.0), cum[got]
-    assert np.isfinite(x64[got]) and lo - 1e-5 <= float(r) < hi + 1e-5, f"step {g}: {got} [{lo}, {hi}) vs r={r}"
+    lo, hi, _ = _cdf_interval(x, got)
+    assert _in_cdf_interval(x, got, r), f"step {g}: {got} [{lo}, {hi}) vs r={r}"
 
 
 def test_device_sampler_temperature_only():

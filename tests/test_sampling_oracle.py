@@ -115,6 +115,17 @@ def test_filters_against_brute_force():
             if cum >= np.float32(p):
                 break
         assert {i for i in range(n) if got[i] != -np.inf} == kept
+        got = x.copy()  # the float64 cut, by the same walk in float64
+        S.apply_top_p(got, p, exact=True)
+        e64 = np.exp(x.astype(np.float64) - float(np.max(x)))
+        p64 = e64 / e64.sum()
+        kept, cum = set(), 0.0
+        for _, i in sorted((-float(p64[i]), i) for i in range(n)):
+            kept.add(i)
+            cum += float(p64[i])
+            if cum >= p:
+                break
+        assert {i for i in range(n) if got[i] != -np.inf} == kept
         r = np.float32(rng.uniform(0, 1))
         cdf = np.cumsum(S._softmax(x), dtype=np.float32)
         want = min(int(np.searchsorted(cdf, r, side="right")), n - 1)
