@@ -1,0 +1,69 @@
+// Batched decode GEMV (2..16 sequences) over tile-ordered weights; see
+// bgemv.hip for the tile layout and the work split.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+namespace rtg {
+
+// QKV epilogue target: q part to q[m][ldq], the new token's k/v parts into
+// the cache at *pos_dev. q == nullptr selects the plain epilogues.
+struct BgemvQkv {
+  float* q;
+  int ldq;
+  int d;
+  KvDst kv;
+  const int* pos_dev;
+};
+
+struct BgemvArgs {
+  const float* X;  // [M][ldx] f32 inputs, M <= 16
+  int ldx, M;
+  const void* Wt;  // tile-ordered weights (launch_tile_weights)
+  int wtype, N, K;
+  const float* bias;  // [N] or null
+  float* C;           // [M][ldc] output (plain epilogues)
+  long ldc;
+  int epi;
+  BgemvQkv qkv;
+  // LayerNorm folded in (ln_g set): x is scaled by ln_g[k] as it is read and
+  // the epilogue computes inv_std * (acc - mean * ln_s[n]) before the bias
+  // (then the folded constant c[n]). The statistics of input row m come from
+  // the partials the kernel that wrote x left in ln_part[g][m] = (mean, M2)
+  // over columns [g * ln_cols, (g + 1) * ln_cols) of K, g < ln_groups <= 128.
+  const float* ln_g;
+  const float* ln_s;
+  const float* ln_part;
+  int ln_groups, ln_cols;
+  float eps;
+  // Residual epilogue only: writes those partials for the rows it wrote,
+  // stats_part[g][m] for its panel groups g (plan.groups * 32 floats), with
+  // groups of 16 * plan.npw columns.
+  float* stats_part;
+  float* part;    // workspace of bgemv_work_floats(plan) floats when plan.S > 1
+  unsigned* cnt;  // plan.groups zeroed counters when plan.S > 1 (left zeroed)
+  int S, ktc;     // filled in from the plan
+};
+
+struct BgemvPlan {
+  int npw;     // 16-row panels per wave
+  int S;       // workgroups per panel group (k splits)
+  int ktc;     // k-tiles per wave
+  int groups;  // panel groups
+};
+
+// Bytes of the tile-ordered copy of W^T[N][K] (rows padded to 16).
+size_t tiled_weight_bytes(int N, int K, int wtype);
+// Writes the tile-ordered copy of a row-major W^T[N][K] in storage type wtype.
+bool launch_tile_weights(hipStream_t s, const void* src, int wtype, int N, int K, void* dst);
+// Work split for one GEMV shape; npw_force / s_force > 0 override the choice.
+BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force = 0, int s_force = 0);
+size_t bgemv_work_floats(const BgemvPlan& pl);
+bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a);
+// LayerNorm statistics partials of rows x[r][0, d) as one group of width d:
+// part[r] = (mean, M2) (the ln_part of a following GEMV, ln_groups = 1).
+void launch_row_stats(hipStream_t s, const float* x, int rows, int d, float* part);
+
+}  // namespace rtg

@@ -25,7 +25,6 @@ const void* kernel_1280_50257_f32();
 const void* kernel_1600_50257_bf16();
 }  // namespace pk
 
-namespace {
 // LayerNorm folded into the GEMV that follows it: for output row r of
 // W^T[N][K] (row r contiguous), s[r] = sum_k W[r][k] g[k] and
 // c[r] = bias[r] + sum_k W[r][k] b[k], accumulated in double. One wave per row.
@@ -57,6 +56,7 @@ bool ln_fold(const void* W, int wtype, int N, int K, const float* g, const float
   return hipGetLastError() == hipSuccess;
 }
 
+namespace {
 struct Inst {
   int d, v, wtype;
   const void* (*fn)();

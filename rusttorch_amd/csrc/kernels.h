@@ -73,6 +73,13 @@ void launch_kv_append(hipStream_t s, const float* qkv, int S, int T, int past, K
 void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past, const float* kc, const float* vc,
                          int n_head, int n_pos, int d, float* out);
 
+// LayerNorm folded into the GEMV that follows it (computed once per model,
+// accumulated in double): for output row r of W^T[N][K],
+// s[r] = sum_k W[r][k] g[k] and c[r] = bias[r] + sum_k W[r][k] b[k]
+// (bias may be null), so LN(x) W + bias = inv_std (W (x g) - mean s) + c.
+bool ln_fold(const void* W, int wtype, int N, int K, const float* g, const float* b, const float* bias, float* s,
+             float* c);
+
 // bf16 conversion / transposition used once at model load.
 // Token choice of one decode step on the device (sampling.hip).
 struct SampleParams {

@@ -19,6 +19,7 @@
 
 #include "../../include/rtgpu.h"
 #include "decode_persistent.h"
+#include "bgemv.h"
 #include "kernels.h"
 #include "safetensors_reader.h"
 
@@ -79,6 +80,23 @@ struct LayerW {
   float *ln1w, *ln1b, *ln2w, *ln2b;
 };
 
+// Tile-ordered copies of the decode GEMV weights and the folded LayerNorm
+// constants for the batched decode step (bgemv.h), built on first use.
+struct BatchedWeights {
+  void* arena = nullptr;
+  struct Layer {
+    const void *qkv, *proj, *fc, *mproj;  // tiled W^T
+    const float *sq, *cq, *sf, *cf;       // LN1 into c_attn, LN2 into c_fc
+  };
+  std::vector<Layer> layers;
+  const void* lm = nullptr;  // tiled wte (the tied LM head)
+  const float *sl = nullptr, *cl = nullptr;  // ln_f into the LM head
+  BgemvPlan pq{}, pp{}, pf{}, pm{}, pl{};    // c_attn, attn c_proj, c_fc, mlp c_proj, LM head
+  ~BatchedWeights() {
+    if (arena) hipFree(arena);
+  }
+};
+
 struct rtg_model {
   rtg_config cfg;
   int hd = 0;
@@ -92,6 +110,8 @@ struct rtg_model {
   std::vector<LayerW> layers;
   size_t nparams = 0;
   PersistentPlan* pplan = nullptr;
+  std::mutex bw_mu;
+  std::unique_ptr<BatchedWeights> bw;
   // Pool of caches reused by the generate entry points (keyed by batch).
   std::mutex pool_mu;
   std::multimap<size_t, rtg_cache*> pool;
@@ -128,6 +148,11 @@ struct rtg_cache {
   hipGraphExec_t graph_exec = nullptr;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   PersistentState* pstate = nullptr;
+  // batched decode step (bgemv): split-k partials and counters, per-group
+  // LayerNorm statistics partials of the residual stream
+  float* bg_part = nullptr;
+  unsigned* bg_cnt = nullptr;
+  float* bg_spart = nullptr;
 };
 
 static void free_work(rtg_cache* c) {
@@ -252,6 +277,173 @@ static void enqueue_prefill(rtg_cache* c, const uint32_t* ids_dev, size_t S, siz
   }
 }
 
+// ---- batched decode step on the tile-ordered GEMV (bgemv.h) ----
+
+// The batched step needs every GEMV's K to be a whole number of k-tiles and at
+// most 16 sequences; other shapes keep the per-op kernels below.
+static bool batched_ok(const rtg_model* m, size_t B) {
+  const size_t tk = m->wtype == W_F32 ? 16 : 32;
+  // (the LayerNorm statistics of a row come in at most 128 panel groups)
+  return B >= 1 && B <= 16 && m->cfg.n_embd % tk == 0 && m->cfg.n_embd <= 2048;
+}
+
+// Builds the model's tile-ordered weight copies and folded LayerNorm constants
+// (once; callers may race, the mutex serialises them).
+static const BatchedWeights* ensure_batched(const rtg_model* mc) {
+  rtg_model* m = const_cast<rtg_model*>(mc);
+  std::lock_guard<std::mutex> g(m->bw_mu);
+  if (m->bw) return m->bw.get();
+  const int d = (int)m->cfg.n_embd, V = (int)m->cfg.vocab_size, L = (int)m->layers.size(), wt = m->wtype;
+  std::unique_ptr<BatchedWeights> bw(new BatchedWeights());
+  const size_t tq = tiled_weight_bytes(3 * d, d, wt), tp = tiled_weight_bytes(d, d, wt);
+  const size_t tf = tiled_weight_bytes(4 * d, d, wt), tm = tiled_weight_bytes(d, 4 * d, wt);
+  const size_t tl = tiled_weight_bytes(V, d, wt);
+  const size_t per_layer = align_up(tq, 256) + align_up(tp, 256) + align_up(tf, 256) + align_up(tm, 256);
+  const size_t fold_layer = (size_t)(2 * 3 * d + 2 * 4 * d) * 4;
+  const size_t total = per_layer * L + align_up(tl, 256) + align_up(fold_layer, 256) * L + align_up((size_t)2 * V * 4, 256);
+  HIPX(hipDeviceSynchronize());
+  HIPX(hipMalloc(&bw->arena, total));
+  char* p = static_cast<char*>(bw->arena);
+  auto take = [&](size_t n) {
+    char* r = p;
+    p += align_up(n, 256);
+    return r;
+  };
+  auto tile = [&](const void* src, int N, int K, size_t bytes) {
+    void* dst = take(bytes);
+    if (!launch_tile_weights(nullptr, src, wt, N, K, dst)) throw HipError{"tile_weights launch failed"};
+    return (const void*)dst;
+  };
+  for (int l = 0; l < L; ++l) {
+    const LayerW& W = m->layers[l];
+    BatchedWeights::Layer bl{};
+    bl.qkv = tile(W.wqkv, 3 * d, d, tq);
+    bl.proj = tile(W.waproj, d, d, tp);
+    bl.fc = tile(W.wfc, 4 * d, d, tf);
+    bl.mproj = tile(W.wmproj, d, 4 * d, tm);
+    float* f = reinterpret_cast<float*>(take(fold_layer));
+    float *sq = f, *cq = f + 3 * d, *sf = f + 6 * d, *cf = f + 10 * d;
+    if (!ln_fold(W.wqkv, wt, 3 * d, d, W.ln1w, W.ln1b, W.bqkv, sq, cq) ||
+        !ln_fold(W.wfc, wt, 4 * d, d, W.ln2w, W.ln2b, W.bfc, sf, cf))
+      throw HipError{"ln_fold launch failed"};
+    bl.sq = sq; bl.cq = cq; bl.sf = sf; bl.cf = cf;
+    bw->layers.push_back(bl);
+  }
+  bw->lm = tile(m->wte, V, d, tl);
+  float* fl = reinterpret_cast<float*>(take((size_t)2 * V * 4));
+  if (!ln_fold(m->wte, wt, V, d, m->lnfw, m->lnfb, nullptr, fl, fl + V)) throw HipError{"ln_fold launch failed"};
+  bw->sl = fl;
+  bw->cl = fl + V;
+  HIPX(hipDeviceSynchronize());
+  bw->pq = bgemv_plan(3 * d, d, wt);
+  bw->pp = bgemv_plan(d, d, wt);
+  bw->pf = bgemv_plan(4 * d, d, wt);
+  bw->pm = bgemv_plan(d, 4 * d, wt);
+  bw->pl = bgemv_plan(V, d, wt);
+  m->bw = std::move(bw);
+  return m->bw.get();
+}
+
+// The cache's workspace for the batched step (allocated once per cache).
+static void ensure_bg_work(rtg_cache* c, const BatchedWeights* bw) {
+  if (c->bg_part) return;
+  size_t part = 1, groups = 1;
+  for (const BgemvPlan* pl : {&bw->pq, &bw->pp, &bw->pf, &bw->pm, &bw->pl}) {
+    part = std::max(part, bgemv_work_floats(*pl));
+    groups = std::max(groups, (size_t)pl->groups);
+  }
+  HIPX(hipMalloc(&c->bg_part, part * 4));
+  HIPX(hipMalloc(&c->bg_cnt, groups * 4));
+  HIPX(hipMalloc(&c->bg_spart, groups * 16 * 2 * 4));
+  HIPX(hipMemsetAsync(c->bg_cnt, 0, groups * 4, c->stream));
+  HIPX(hipStreamSynchronize(c->stream));
+}
+
+// Prepares the graph path's decode step of a cache (before any capture).
+static void prepare_decode(rtg_cache* c) {
+  if (c->pstate || !batched_ok(c->m, c->batch)) return;
+  ensure_bg_work(c, ensure_batched(c->m));
+}
+
+// One decode step for B sequences: per layer four tile-ordered GEMVs with
+// LayerNorm folded into c_attn / c_fc / the LM head (row statistics written by
+// the residual epilogues) and the cached attention; forward_cached with one
+// token per sequence (gpt2.rs:376-396, 477-538).
+static void enqueue_decode_step_batched(rtg_cache* c) {
+  const rtg_model* m = c->m;
+  const BatchedWeights* bw = m->bw.get();
+  const int d = (int)m->cfg.n_embd, V = (int)m->cfg.vocab_size, B = (int)c->batch;
+  const float eps = m->cfg.layer_norm_epsilon;
+  hipStream_t s = c->stream;
+  auto base = [&]() {
+    BgemvArgs a{};
+    a.M = B;
+    a.wtype = m->wtype;
+    a.part = c->bg_part;
+    a.cnt = c->bg_cnt;
+    a.eps = eps;
+    return a;
+  };
+  auto run = [&](const BgemvPlan& pl, const BgemvArgs& a) {
+    if (!launch_bgemv(s, pl, a)) throw HipError{"bgemv launch failed"};
+  };
+  launch_embed(s, m->wte, m->wtype, m->wpe, c->token_dev, B, 1, 0, c->pos_dev, d, c->x);
+  launch_row_stats(s, c->x, B, d, c->bg_spart);
+  // shape of the statistics partials the last residual writer left
+  int st_groups = 1, st_cols = d;
+  auto ln_in = [&](BgemvArgs& a, const float* g, const float* sv) {
+    a.ln_g = g; a.ln_s = sv; a.ln_part = c->bg_spart; a.ln_groups = st_groups; a.ln_cols = st_cols;
+  };
+  auto resid_out = [&](BgemvArgs& a, const BgemvPlan& pl) {
+    a.stats_part = c->bg_spart;
+    st_groups = pl.groups;
+    st_cols = 16 * pl.npw;
+  };
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const LayerW& L = m->layers[l];
+    const BatchedWeights::Layer& T = bw->layers[l];
+    KvDst kv = kv_layer(c, l);
+    {  // LN1 + c_attn; k/v of the new token into the cache
+      BgemvArgs a = base();
+      a.X = c->x; a.ldx = d; a.Wt = T.qkv; a.N = 3 * d; a.K = d; a.bias = T.cq;
+      ln_in(a, L.ln1w, T.sq);
+      a.epi = EPI_BIAS;
+      a.qkv = BgemvQkv{c->qkv, d, d, kv, c->pos_dev};
+      run(bw->pq, a);
+    }
+    launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d, c->att_work);
+    {  // attention c_proj + residual; statistics partials for LN2
+      BgemvArgs a = base();
+      a.X = c->att; a.ldx = d; a.Wt = T.proj; a.N = d; a.K = d; a.bias = L.baproj;
+      a.C = c->x; a.ldc = d; a.epi = EPI_BIAS_RESID;
+      resid_out(a, bw->pp);
+      run(bw->pp, a);
+    }
+    {  // LN2 + c_fc + gelu_new
+      BgemvArgs a = base();
+      a.X = c->x; a.ldx = d; a.Wt = T.fc; a.N = 4 * d; a.K = d; a.bias = T.cf;
+      ln_in(a, L.ln2w, T.sf);
+      a.C = c->h; a.ldc = 4 * d; a.epi = EPI_BIAS_GELU;
+      run(bw->pf, a);
+    }
+    {  // mlp c_proj + residual; statistics partials for the next LayerNorm
+      BgemvArgs a = base();
+      a.X = c->h; a.ldx = 4 * d; a.Wt = T.mproj; a.N = d; a.K = 4 * d; a.bias = L.bmproj;
+      a.C = c->x; a.ldc = d; a.epi = EPI_BIAS_RESID;
+      resid_out(a, bw->pm);
+      run(bw->pm, a);
+    }
+  }
+  {  // ln_f + tied LM head (gpt2.rs:392-396)
+    BgemvArgs a = base();
+    a.X = c->x; a.ldx = d; a.Wt = bw->lm; a.N = V; a.K = d; a.bias = bw->cl;
+    ln_in(a, m->lnfw, bw->sl);
+    a.C = c->logits; a.ldc = V; a.epi = EPI_BIAS;
+    run(bw->pl, a);
+  }
+  launch_argmax(s, c->logits, V, B, V, c->keys);
+}
+
 // One decode step for all B sequences of the cache, reading the token from
 // token_dev and the position from pos_dev (both device-resident), writing the
 // argmax token back to token_dev and ids_dev[b][step]. Capturable.
@@ -263,6 +455,8 @@ static void enqueue_decode_step(rtg_cache* c) {
   const int P = (int)m->cfg.n_positions;
   if (c->pstate) {
     HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/false));
+  } else if (c->bg_part) {
+    enqueue_decode_step_batched(c);
   } else {
     launch_embed(s, m->wte, m->wtype, m->wpe, c->token_dev, B, 1, 0, c->pos_dev, d, c->x);
     for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -326,8 +520,18 @@ static void forward_cached_impl(rtg_cache* c, const uint32_t* ids, size_t n, flo
   const size_t B = c->batch, V = m->cfg.vocab_size;
   ensure_rows(c, B * n);
   ensure_logits(c, B * n);
-  HIPX(hipMemcpyAsync(c->ids_in, ids, B * n * 4, hipMemcpyHostToDevice, c->stream));
-  enqueue_prefill(c, c->ids_in, B, n, c->len, 0);
+  if (n == 1 && B >= 2 && !c->pstate && batched_ok(m, B)) {
+    // one new token per sequence: the batched decode step (the same kernels
+    // generate_cached_batched replays), its token read from token_dev at
+    // position *pos_dev = past
+    prepare_decode(c);
+    HIPX(hipMemcpyAsync(c->token_dev, ids, B * 4, hipMemcpyHostToDevice, c->stream));
+    set_counters(c, (int)c->len, 0);
+    enqueue_decode_step(c);
+  } else {
+    HIPX(hipMemcpyAsync(c->ids_in, ids, B * n * 4, hipMemcpyHostToDevice, c->stream));
+    enqueue_prefill(c, c->ids_in, B, n, c->len, 0);
+  }
   if (logits_out) HIPX(hipMemcpyAsync(logits_out, c->logits, B * n * V * 4, hipMemcpyDeviceToHost, c->stream));
   HIPX(hipStreamSynchronize(c->stream));
   c->len += n;
@@ -385,6 +589,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
                                         c->ids_dev, c->step_dev);
     destroy_graph(c);  // the step graph changes shape
   }
+  prepare_decode(c);
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
   HIPX(hipEventRecord(c->ev[0], s));
   enqueue_prefill(c, c->ids_in, B, n, 0, 0);
@@ -766,7 +971,8 @@ void rtg_cache_destroy(rtg_cache* c) {
   if (c->pstate) persistent_state_destroy(c->pstate);
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
-                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits})
+                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits,
+                  (void*)c->bg_part, (void*)c->bg_cnt, (void*)c->bg_spart})
     if (p) hipFree(p);
   for (auto e : c->ev)
     if (e) hipEventDestroy(e);

@@ -373,6 +373,37 @@ def test_small_batched_matches_single(O):
         assert om.generate_cached(prompts[b], 12) == out[b, : n + 12].tolist()
 
 
+def _batched_step_logits(O, sd, sh, m, B, n_prompt, n_steps, stream, what):
+    """forward_cached with one new token per sequence (B >= 2 runs the
+    batched decode step: tile-ordered GEMVs with LayerNorm folded in, the
+    row statistics written by the residual epilogues) against the oracle,
+    sequence by sequence, for n_steps greedy steps after a prefill."""
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    prompts = np.stack([synth.make_tokens(n_prompt, sh.vocab_size, stream=stream + b) for b in range(B)])
+    c = m.new_cache(batch=B)
+    m.forward_cached_batched(prompts, c)
+    ocs = [om.new_cache() for _ in range(B)]
+    nxt = []
+    for b in range(B):
+        lg = om.forward_cached(prompts[b], ocs[b])
+        nxt.append(O.argmax(lg[-1]))
+    for t in range(n_steps):
+        toks = np.array(nxt, dtype=np.uint32).reshape(B, 1)
+        lg = m.forward_cached_batched(toks, c)
+        nxt = []
+        for b in range(B):
+            ref = om.forward_cached([int(toks[b, 0])], ocs[b])
+            assert_logits_close(lg[b], ref, f"{what} step {t} seq {b}")
+            nxt.append(O.argmax(ref[0]))
+
+
+def test_small_batched_decode_logits(O):
+    """GPT-2 small, 4 sequences: the batched decode step's logits (k split
+    over workgroups in c_proj / mlp.c_proj, 48 statistics groups per merge)."""
+    sd, sh, m = gpu_model("small")
+    _batched_step_logits(O, sd, sh, m, 4, 20, 3, 470, "small b=4")
+
+
 def test_long_prefill_attention_blocks(O):
     """Prefill attention over many key blocks, several query blocks, a past
     length that is not a block multiple and a second chunk appended to a
@@ -471,6 +502,9 @@ def test_xl_bf16_decode(O):
     om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
     for b in range(2):
         assert out[b].tolist() == om.generate_cached(prompts[b], 6)
+    # the batched decode step's logits with bf16 tiles (16 sequences: every
+    # row of the MFMA tile in use)
+    _batched_step_logits(O, sd, sh, m, 16, 4, 1, 480, "xl bf16 b=16")
     m.close()
 
 
