@@ -47,12 +47,10 @@ void launch_gemv(hipStream_t s, int B, const void* W, int wtype, const float* bi
 void launch_gemv_qkv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
                      float* q, int ldq, int d, KvDst kv, const int* pos_dev);
 
-// Decode attention over the cache for positions [0, *pos_dev] (gpt2.rs:772-834).
-// Decode attention; `work` (attn_decode_work_floats floats, or null for the
-// single-block kernel) holds the per-split partials of the head_dim-64 path.
-size_t attn_decode_work_floats(int B, int n_head, int n_pos);
+// Decode attention over the cache for positions [0, *pos_dev] (gpt2.rs:772-834),
+// one new token per sequence.
 void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc,
-                        int n_head, int n_pos, const int* pos_dev, float* out, int ldo, float* work);
+                        int n_head, int n_pos, const int* pos_dev, float* out, int ldo);
 
 // Greedy argmax over rows of logits (gpt2.rs:858-868) into packed keys.
 void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V, unsigned long long* keys);

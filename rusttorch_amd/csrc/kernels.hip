@@ -337,14 +337,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
   if (tid < hd) out[(size_t)b * ldo + h * hd + tid] = (pv[tid] + pv[64 + tid]) + (pv[128 + tid] + pv[192 + tid]);
 }
 
-// Decode attention for head_dim 64, split over positions (one new token per
-// sequence, gpt2.rs:772-834): block (h, b, sp) takes positions
-// [128 sp, 128 sp + 128), 32 per wave; 16 lanes per position (4 dims each)
-// with the 16-lane sums in DPP, all K/V rows of a wave loaded at once. Each
-// block writes its partial softmax (m, l, o[64]); the combine kernel merges
-// the partials of the splits that exist at this length.
-constexpr int AD_ROWS = 128;
-constexpr int AD_ITEM = 2 + 64;
+constexpr int AD_ITEM = 2 + 64;  // per-wave softmax state: m, l, o[64]
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_row(float v) {
@@ -378,50 +371,83 @@ __device__ __forceinline__ float row16_sum_k(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void attn_decode_split_kernel(const float* __restrict__ q, int ldq,
-                                                                const float* __restrict__ kc,
-                                                                const float* __restrict__ vc, int H, int P,
-                                                                const int* __restrict__ pos_dev,
-                                                                float* __restrict__ part, int nsmax) {
-  __shared__ float wp[4][AD_ITEM];
-  const int h = blockIdx.x, b = blockIdx.y, sp = blockIdx.z;
+// Decode attention for head_dim 64 in one kernel (one new token per
+// sequence, gpt2.rs:772-834): block (h, b) of NWV waves; wave w takes the
+// 16-row windows w, w + NWV, ... of positions [0, len), each window's K/V
+// rows loaded while the previous one is computed (two register sets), with an
+// online softmax per wave (16 lanes per row, 4 dims each, DPP row sums). The
+// wave states (m, l, o) merge in LDS in wave order; the block writes o / l.
+constexpr int AF_RG = 4;  // row groups of 4 rows per window
+
+__device__ __forceinline__ void af_load(const float* Kh, const float* Vh, int r0, int len, int grp,
+                                        float4 (&k4)[AF_RG], float4 (&v4)[AF_RG]) {
+#pragma unroll
+  for (int t = 0; t < AF_RG; ++t) {
+    const int r = min(r0 + 4 * t + grp, len - 1);
+    k4[t] = *reinterpret_cast<const float4*>(Kh + (size_t)r * 64);
+    v4[t] = *reinterpret_cast<const float4*>(Vh + (size_t)r * 64);
+  }
+}
+
+__device__ __forceinline__ void af_window(const float4 (&k4)[AF_RG], const float4 (&v4)[AF_RG], const float4& q4,
+                                          int r0, int len, int grp, float& m, float& lsum, float4& o4) {
+  float s[AF_RG];
+  float mb = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < AF_RG; ++t) {
+    const float dot = row16_sum_k(q4.x * k4[t].x + q4.y * k4[t].y + q4.z * k4[t].z + q4.w * k4[t].w);
+    s[t] = r0 + 4 * t + grp < len ? dot * 0.125f : -INFINITY;  // 1 / sqrt(64)
+    mb = fmaxf(mb, s[t]);
+  }
+  mb = xor32_max_k(xor16_max_k(mb));
+  const float mn = fmaxf(m, mb);
+  const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+  lsum *= corr;
+  o4.x *= corr;
+  o4.y *= corr;
+  o4.z *= corr;
+  o4.w *= corr;
+#pragma unroll
+  for (int t = 0; t < AF_RG; ++t) {
+    const float p = s[t] == -INFINITY ? 0.f : expf(s[t] - mn);
+    lsum += p;
+    o4.x += p * v4[t].x;
+    o4.y += p * v4[t].y;
+    o4.z += p * v4[t].z;
+    o4.w += p * v4[t].w;
+  }
+  m = mn;
+}
+
+template <int NWV>
+__global__ __launch_bounds__(64 * NWV) void attn_decode_fused_kernel(const float* __restrict__ q, int ldq,
+                                                                    const float* __restrict__ kc,
+                                                                    const float* __restrict__ vc, int H, int P,
+                                                                    const int* __restrict__ pos_dev,
+                                                                    float* __restrict__ out, int ldo) {
+  constexpr int WR = 4 * AF_RG;  // rows per window
+  __shared__ float wp[NWV][AD_ITEM];
+  const int h = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, grp = lane >> 4, dq = (lane & 15) * 4;
   const int len = *pos_dev + 1;
-  if (sp * AD_ROWS >= len) return;  // no rows: the combine kernel skips this split
   const size_t head_off = ((size_t)b * H + h) * (size_t)P * 64;
-  const int j0 = sp * AD_ROWS + wave * 32;
-  const int n = min(32, len - j0);  // this wave's rows (<= 0: none)
+  const float* Kh = kc + head_off + dq;
+  const float* Vh = vc + head_off + dq;
   float m = -INFINITY, lsum = 0.f;
   float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (n > 0) {
+  const int nwin = (len + WR - 1) / WR;
+  if (wave < nwin) {
     const float4 q4 = *reinterpret_cast<const float4*>(q + (size_t)b * ldq + h * 64 + dq);
-    const float* Kh = kc + head_off + (size_t)j0 * 64 + dq;
-    const float* Vh = vc + head_off + (size_t)j0 * 64 + dq;
-    float4 k4[8], v4[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int r = min(4 * t + grp, n - 1);
-      k4[t] = *reinterpret_cast<const float4*>(Kh + (size_t)r * 64);
-      v4[t] = *reinterpret_cast<const float4*>(Vh + (size_t)r * 64);
-    }
-    float s[8];
-    float mb = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const float dot = row16_sum_k(q4.x * k4[t].x + q4.y * k4[t].y + q4.z * k4[t].z + q4.w * k4[t].w);
-      s[t] = 4 * t + grp < n ? dot * 0.125f : -INFINITY;  // 1 / sqrt(64)
-      mb = fmaxf(mb, s[t]);
-    }
-    mb = xor32_max_k(xor16_max_k(mb));
-    m = mb;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const float p = s[t] == -INFINITY ? 0.f : expf(s[t] - m);
-      lsum += p;
-      o4.x += p * v4[t].x;
-      o4.y += p * v4[t].y;
-      o4.z += p * v4[t].z;
-      o4.w += p * v4[t].w;
+    float4 ka[AF_RG], va[AF_RG], kb[AF_RG], vb[AF_RG];
+    af_load(Kh, Vh, wave * WR, len, grp, ka, va);
+    for (int w = wave; w < nwin; w += 2 * NWV) {
+      const int wn = w + NWV;
+      if (wn < nwin) af_load(Kh, Vh, wn * WR, len, grp, kb, vb);
+      af_window(ka, va, q4, w * WR, len, grp, m, lsum, o4);
+      if (wn >= nwin) break;
+      const int wn2 = wn + NWV;
+      if (wn2 < nwin) af_load(Kh, Vh, wn2 * WR, len, grp, ka, va);
+      af_window(kb, vb, q4, wn * WR, len, grp, m, lsum, o4);
     }
     // sum over the 4 row groups
     lsum = xor32_sum_k(xor16_sum_k(lsum));
@@ -437,61 +463,36 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(const float* __r
     wp[wave][5 + dq] = o4.w;
   }
   if (lane == 0) {
-    wp[wave][0] = m;
+    wp[wave][0] = m;  // -inf (and l = 0) for a wave without rows
     wp[wave][1] = lsum;
   }
   __syncthreads();
   if (tid < 64) {
     float M = -INFINITY;
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wp[w][0]);
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) M = fmaxf(M, wp[w][0]);
     float Ls = 0.f, o = 0.f;
-    for (int w = 0; w < 4; ++w) {
-      if (wp[w][0] == -INFINITY) continue;
-      const float f = expf(wp[w][0] - M);
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) {
+      const float mw = wp[w][0];
+      const float f = mw == -INFINITY ? 0.f : expf(mw - M);
       Ls += wp[w][1] * f;
       o += wp[w][2 + tid] * f;
     }
-    float* dst = part + (((size_t)b * H + h) * nsmax + sp) * AD_ITEM;
-    dst[2 + tid] = o;
-    if (tid == 0) {
-      dst[0] = M;
-      dst[1] = Ls;
-    }
+    out[(size_t)b * ldo + h * 64 + tid] = o / Ls;
   }
-}
-
-__global__ __launch_bounds__(64) void attn_decode_combine_kernel(const float* __restrict__ part, int H, int nsmax,
-                                                                 const int* __restrict__ pos_dev,
-                                                                 float* __restrict__ out, int ldo) {
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int ns = (*pos_dev + 1 + AD_ROWS - 1) / AD_ROWS;
-  const float* it = part + ((size_t)b * H + h) * nsmax * AD_ITEM;
-  float M = -INFINITY;
-  for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, it[sp * AD_ITEM]);
-  float Ls = 0.f, o = 0.f;
-  for (int sp = 0; sp < ns; ++sp) {
-    const float ms = it[sp * AD_ITEM];
-    if (ms == -INFINITY) continue;
-    const float f = expf(ms - M);
-    Ls += it[sp * AD_ITEM + 1] * f;
-    o += it[sp * AD_ITEM + 2 + tid] * f;
-  }
-  out[(size_t)b * ldo + h * 64 + tid] = o / Ls;
-}
-
-size_t attn_decode_work_floats(int B, int n_head, int n_pos) {
-  return (size_t)B * n_head * ((n_pos + AD_ROWS - 1) / AD_ROWS) * AD_ITEM;
 }
 
 void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc, int n_head,
-                        int n_pos, const int* pos_dev, float* out, int ldo, float* work) {
+                        int n_pos, const int* pos_dev, float* out, int ldo) {
   // head_dim = ldq-independent: derived by the caller into n_head via ldo.
   const int hd = ldo / n_head;
-  if (hd == 64 && work) {
-    const int nsmax = (n_pos + AD_ROWS - 1) / AD_ROWS;
-    attn_decode_split_kernel<<<dim3(n_head, B, nsmax), 256, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, work,
-                                                                    nsmax);
-    attn_decode_combine_kernel<<<dim3(n_head, B), 64, 0, s>>>(work, n_head, nsmax, pos_dev, out, ldo);
+  if (hd == 64) {
+    // 16 waves per (head, sequence) while there are fewer pairs than CUs
+    if (n_head * B < 256)
+      attn_decode_fused_kernel<16><<<dim3(n_head, B), 1024, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, out, ldo);
+    else
+      attn_decode_fused_kernel<8><<<dim3(n_head, B), 512, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, out, ldo);
     return;
   }
   const size_t smem = (336 + (size_t)n_pos) * sizeof(float);

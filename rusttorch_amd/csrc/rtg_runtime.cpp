@@ -137,7 +137,6 @@ struct rtg_cache {
   uint32_t* token_dev = nullptr;
   uint32_t* ids_dev = nullptr;   // [B][P] generated ids
   uint32_t* ids_in = nullptr;    // [B*P] prompt ids
-  float* att_work = nullptr;     // per-split partials of decode attention
   // work buffers, capacity in rows
   size_t rows_cap = 0;
   float *x = nullptr, *ln = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
@@ -212,7 +211,6 @@ static rtg_cache* cache_create(const rtg_model* m, size_t batch) {
     HIPX(hipMalloc(&c->token_dev, std::max<size_t>(batch, 1) * 4));
     HIPX(hipMalloc(&c->ids_dev, std::max<size_t>(batch * P, 1) * 4));
     HIPX(hipMalloc(&c->ids_in, std::max<size_t>(batch * P, 1) * 4));
-    HIPX(hipMalloc(&c->att_work, std::max<size_t>(attn_decode_work_floats((int)batch, (int)H, (int)P), 1) * 4));
     for (auto& e : c->ev) HIPX(hipEventCreate(&e));
     HIPX(hipMemsetAsync(c->pos_dev, 0, 256, c->stream));
     HIPX(hipMemsetAsync(c->step_dev, 0, 256, c->stream));
@@ -411,7 +409,7 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
       a.qkv = BgemvQkv{c->qkv, d, d, kv, c->pos_dev};
       run(bw->pq, a);
     }
-    launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d, c->att_work);
+    launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d);
     {  // attention c_proj + residual; statistics partials for LN2
       BgemvArgs a = base();
       a.X = c->att; a.ldx = d; a.Wt = T.proj; a.N = d; a.K = d; a.bias = L.baproj;
@@ -464,7 +462,7 @@ static void enqueue_decode_step(rtg_cache* c) {
       KvDst kv = kv_layer(c, l);
       launch_layernorm(s, c->x, L.ln1w, L.ln1b, eps, B, d, c->ln);
       launch_gemv_qkv(s, B, L.wqkv, m->wtype, L.bqkv, c->ln, d, c->qkv, d, d, kv, c->pos_dev);
-      launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d, c->att_work);
+      launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d);
       launch_gemv(s, B, L.waproj, m->wtype, L.baproj, c->att, d, c->x, d, d, d, EPI_BIAS_RESID);
       launch_layernorm(s, c->x, L.ln2w, L.ln2b, eps, B, d, c->ln);
       launch_gemv(s, B, L.wfc, m->wtype, L.bfc, c->ln, d, c->h, 4 * d, 4 * d, d, EPI_BIAS_GELU);
@@ -971,7 +969,7 @@ void rtg_cache_destroy(rtg_cache* c) {
   if (c->pstate) persistent_state_destroy(c->pstate);
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
-                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->att_work, (void*)c->logits,
+                  (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->logits,
                   (void*)c->bg_part, (void*)c->bg_cnt, (void*)c->bg_spart})
     if (p) hipFree(p);
   for (auto e : c->ev)
