@@ -599,10 +599,12 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev);
   sample(c->logits + (n - 1) * V);
   HIPX(hipEventRecord(c->ev[1], s));
-  // RTG_NO_GRAPH=1: enqueue each step's kernels directly instead of replaying
-  // the captured step graph (for per-kernel profiling; same results).
+  // The persistent step (one kernel) is launched directly: replaying it as a
+  // one-node graph was measured to leave ~8 us between launches instead of ~1.
+  // RTG_NO_GRAPH=1 does the same for the batched step's kernels (for
+  // per-kernel profiling; same results).
   const char* ng = getenv("RTG_NO_GRAPH");
-  if (ng && ng[0] == '1') {
+  if (c->pstate || (ng && ng[0] == '1')) {
     for (size_t i = 1; i < steps; ++i) {
       enqueue_decode_step(c);
       sample(c->logits);
