@@ -143,7 +143,8 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   auto region = [](int n) { return pk::G * pk::slot_words((n + pk::G - 1) / pk::G); };
   p.o_qkv = 0;
   p.o_att = region(3 * d);
-  p.o_x2 = p.o_att + pk::MAX_ITEMS * pk::ITEM_SLOT;
+  p.o_head = p.o_att + pk::MAX_ITEMS * pk::ITEM_SLOT;  // merged outputs of chunked heads
+  p.o_x2 = p.o_head + H * pk::ITEM_SLOT;
   p.o_h = p.o_x2 + region(d);
   p.o_x3 = p.o_h + region(4 * d);
   p.lw = p.o_x3 + region(d);

@@ -47,7 +47,7 @@ constexpr int NTHREADS = (1 + NA + NC) * 64;
 constexpr int HD = 64;              // head_dim of every GPT-2 size
 constexpr int CMAX = 16;            // attention chunks per head
 constexpr int ITEM_WORDS = HD + 2;  // o[64], m, l
-constexpr int MAX_ITEMS = 64;       // heads * chunks merged by the consumers
+constexpr int MAX_ITEMS = G;        // heads * chunks: at most one attention item per workgroup
 constexpr int PART_MAX = 1536;      // segment partials per workgroup
 // GEMV phase types, each with its own input-ready counter. A glue wave counts
 // itself once per layer in each; every workgroup owns rows of the FC phase in
@@ -97,7 +97,7 @@ struct Params {
   unsigned* epoch;  // tag of this step; advanced by the last workgroup
   u64* tag;  // tagged words, lw per layer
   long lw;
-  int o_qkv, o_att, o_x2, o_h, o_x3;  // exchange regions of a layer (words)
+  int o_qkv, o_att, o_head, o_x2, o_h, o_x3;  // exchange regions of a layer (words)
   float* logits;
   u64* keys;
   unsigned* err;
@@ -160,7 +160,7 @@ struct Smem {
   float xraw[D];           // residual input of the current layer
   float x2raw[D];          // residual after attention
   float part[PART_MAX];
-  float stage[MAX_ITEMS * ITEM_WORDS];
+  float stage[CMAX * ITEM_WORDS];  // a chunked head's items, on the workgroup that merges them
   float kv_k[KVS * HD], kv_v[KVS * HD];  // K/V rows [j0, j0 + KVS) of this workgroup's item
   float att_part[NATT][ITEM_WORDS];
   float att_q[HD], att_k[HD], att_v[HD];
@@ -928,31 +928,33 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         stage_rows(p.kc + nl, p.vc + nl, h0, min(KVW, h1 - h0), ldsK, ldsV, lane);
       }
     }
+    // ---- a head split into chunks: the workgroup holding its chunk 0 merges
+    //      the chunks' partial softmaxes (m, l, o) and publishes o / l ----
+    if (NCH > 1 && item >= 0 && ic == 0) {
+      glue_fetch<ITEM_WORDS, ITEM_SLOT, CMAX * ITEM_WORDS>(T + p.o_att + (long)ih * NCH * ITEM_SLOT, NCH * ITEM_WORDS,
+                                                          tag, sm.stage, gl, p.err);
+      glue_barrier(sm, gen, lane, p.err);
+      if (leader) {
+        float M = -INFINITY;
+        for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[c * ITEM_WORDS + HD]);
+        float Ls = 0.f, o = 0.f;
+        for (int c = 0; c < NCH; ++c) {
+          const float* it = sm.stage + c * ITEM_WORDS;
+          if (it[HD] == -INFINITY) continue;
+          const float f = expf(it[HD] - M);
+          Ls += it[HD + 1] * f;
+          o += it[lane] * f;
+        }
+        tstore(T + p.o_head + (long)ih * ITEM_SLOT + lane, o / Ls, tag);
+      }
+    }
     // ---- attention projection + residual (gpt2.rs:523-526) ----
     {
       const int row0 = wg * GP::RPW, rows_here = min(GP::RPW, GP::N - row0);
       const float bias = leader && lane < rows_here ? PK_G(float, LP.baproj)[row0 + lane] : 0.f;
-      if (NCH == 1) {
-        // one item per head: the heads' outputs are the projection input
-        glue_fetch<HD, ITEM_SLOT, H * HD>(T + p.o_att, H * HD, tag, sm.in_vec[0], gl, p.err);
-      } else {
-        glue_fetch<ITEM_WORDS, ITEM_SLOT, 8 * NGLUE * 64>(T + p.o_att, items * ITEM_WORDS, tag, sm.stage, gl, p.err);
-        glue_barrier(sm, gen, lane, p.err);
-        // merge the chunks of each head; heads are spread over the glue waves
-        for (int h = gw; h < H; h += NGLUE) {
-          float M = -INFINITY;
-          for (int c = 0; c < NCH; ++c) M = fmaxf(M, sm.stage[(h * NCH + c) * ITEM_WORDS + HD]);
-          float Ls = 0.f, o = 0.f;
-          for (int c = 0; c < NCH; ++c) {
-            const float* it = sm.stage + (h * NCH + c) * ITEM_WORDS;
-            if (it[HD] == -INFINITY) continue;
-            const float f = expf(it[HD] - M);
-            Ls += it[HD + 1] * f;
-            o += it[lane] * f;
-          }
-          sm.in_vec[0][h * HD + lane] = o / Ls;
-        }
-      }
+      // the heads' normalised outputs are the projection input: published by
+      // the attention items themselves (one chunk per head) or by the mergers
+      glue_fetch<HD, ITEM_SLOT, H * HD>(T + (NCH == 1 ? p.o_att : p.o_head), H * HD, tag, sm.in_vec[0], gl, p.err);
       glue_input_done(sm, PH_PROJ, lane);
       if (leader) {
         PK_TRACE(p, tb + 5, lane);
@@ -1077,9 +1079,9 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
 }
 
 // Attention chunking for this step: NCH chunks per head, one per KVS
-// positions (so each chunk fits the LDS stage), at most CMAX and
-// H*NCH <= min(MAX_ITEMS, G). Fewer chunks keep the exchange that every
-// workgroup reads (H*NCH partial softmax items) small.
+// positions (so each chunk fits the LDS stage and each attention wave holds
+// one window, loaded a layer ahead), at most CMAX and H*NCH <= G. Every
+// workgroup then reads only the H merged head outputs.
 template <int H>
 __device__ __host__ __forceinline__ int att_chunks(int len) {
   constexpr int cap0 = CMAX < MAX_ITEMS / H ? CMAX : MAX_ITEMS / H;

@@ -475,6 +475,10 @@ def test_medium_decode(O):
     m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
     print("[gpu] medium parity", flush=True)
     _decode_parity(O, sd, sh, m, 16, 24, 4, stream=400)
+    # configuration c3's long context: 6 attention chunks per head, merged
+    # on the workgroup of chunk 0 before every workgroup reads the heads
+    print("[gpu] medium long-context parity", flush=True)
+    _decode_parity(O, sd, sh, m, 640, 6, 2, stream=401)
     m.close()
 
 
