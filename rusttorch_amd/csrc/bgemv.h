@@ -42,6 +42,9 @@ struct BgemvArgs {
   // stats_part[g][m] for its panel groups g (plan.groups * 32 floats), with
   // groups of 16 * plan.npw columns.
   float* stats_part;
+  // LM head of the persistent step only: per-row packed argmax keys
+  // (gpt2.rs:858-868), updated with a device-scope atomic max.
+  unsigned long long* keys;
   float* part;    // workspace of bgemv_work_floats(plan) floats when plan.S > 1
   unsigned* cnt;  // plan.groups zeroed counters when plan.S > 1 (left zeroed)
   int S, ktc;     // filled in from the plan
@@ -58,8 +61,11 @@ struct BgemvPlan {
 size_t tiled_weight_bytes(int N, int K, int wtype);
 // Writes the tile-ordered copy of a row-major W^T[N][K] in storage type wtype.
 bool launch_tile_weights(hipStream_t s, const void* src, int wtype, int N, int K, void* dst);
-// Work split for one GEMV shape; npw_force / s_force > 0 override the choice.
-BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force = 0, int s_force = 0);
+// Work split for one GEMV shape with nw waves per workgroup; npw_force /
+// s_force > 0 override the choice.
+BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force = 0, int s_force = 0, int nw = 4);
+// The argument checks launch_bgemv makes (shape, workspaces, LayerNorm parts).
+bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a);
 size_t bgemv_work_floats(const BgemvPlan& pl);
 bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a);
 // LayerNorm statistics partials of rows x[r][0, d) as one group of width d:
