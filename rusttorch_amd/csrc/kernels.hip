@@ -466,6 +466,8 @@ void launch_reset_keys(hipStream_t s, int B, unsigned long long* keys) { reset_k
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// (a k-tile of 32 was measured slower: 86 against 106 TF/s on the c4 shapes,
+// its LDS footprint halving the workgroups per CU)
 constexpr int GBM = 128, GBN = 128, GBK = 16, GPAD = 4;
 
 template <int WT>
@@ -478,15 +480,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
 
-  // Global->LDS mapping: 128 rows x 16 k = 512 float4; thread t loads rows
-  // (t >> 2) and (t >> 2) + 64 at k offset (t & 3) * 4.
-  const int lr = tid >> 2, lk = (tid & 3) * 4;
-  float4 ra[2], rw[2];
+  // Global->LDS mapping: 128 rows x GBK k = 32 * GBK float4; thread t loads
+  // rows (t / KC) + RPP * h at k offset (t % KC) * 4, KC = GBK / 4 chunks per
+  // row, RPP = 256 / KC rows per pass, NPS = 128 / RPP passes.
+  constexpr int KC = GBK / 4, RPP = 256 / KC, NPS = GBM / RPP;
+  const int lr = tid / KC, lk = (tid % KC) * 4;
+  float4 ra[NPS], rw[NPS];
 
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int m = m0 + lr + h * 64, n = n0 + lr + h * 64, k = k0 + lk;
+    for (int h = 0; h < NPS; ++h) {
+      const int m = m0 + lr + h * RPP, n = n0 + lr + h * RPP, k = k0 + lk;
       float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vw = make_float4(0.f, 0.f, 0.f, 0.f);
       if (m < M) {
         if (k + 3 < K) {
@@ -520,8 +524,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = lr + h * 64;
+    for (int h = 0; h < NPS; ++h) {
+      const int r = lr + h * RPP;
       As[buf][lk + 0][r] = ra[h].x; As[buf][lk + 1][r] = ra[h].y;
       As[buf][lk + 2][r] = ra[h].z; As[buf][lk + 3][r] = ra[h].w;
       Ws[buf][lk + 0][r] = rw[h].x; Ws[buf][lk + 1][r] = rw[h].y;

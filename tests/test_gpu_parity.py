@@ -502,12 +502,23 @@ def test_medium_decode(O):
 
 
 def test_large_decode(O):
-    """GPT-2 large, f32 (d=1280 persistent decode instance)."""
+    """GPT-2 large, f32 (d=1280 persistent decode instance), and a prefill at
+    configuration c4's widths: 2 sequences x 300 tokens through the 128x128
+    MFMA GEMM (c_attn N=3840, c_fc N=5120, mlp c_proj K=5120, the LM head over
+    50257 rows) and the MFMA causal attention, logits of every row."""
     sh = synth.SHAPES["large"]
     sd = synth.make_weights(sh)
     m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
     print("[gpu] large parity", flush=True)
     _decode_parity(O, sd, sh, m, 8, 12, 2, stream=410)
+    B, n = 2, 300
+    ids = np.stack([synth.make_tokens(n, sh.vocab_size, stream=415 + b) for b in range(B)])
+    c = m.new_cache(batch=B)
+    lg = m.forward_cached_batched(ids, c)
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    for b in range(B):
+        print(f"[gpu] large prefill oracle seq {b}", flush=True)
+        assert_logits_close(lg[b], om.forward_cached(ids[b], om.new_cache()), f"large prefill seq {b}")
     m.close()
 
 
