@@ -10,9 +10,12 @@
 //   tile (p,t) = 1 KiB; lane l = 16q + r holds the 16 bytes
 //                W^T[16p + r][t*TK + q*E .. + E)  (E = 4 f32 / 8 bf16 values),
 //                zeros past row N; tiles stored panel-major, [p][t].
-// MFMA step e of a tile pairs k = t*TK + q*E + e for q = 0..3, so lane l's A
-// operand is x[r][t*TK + q*E + e] and it accumulates D[4q + i][r], i < 4
-// (batch row 4q + i, output row 16p + r).
+// f32 tiles: MFMA step e of a tile pairs k = t*TK + q*E + e for q = 0..3, so
+// lane l's A operand is x[r][t*TK + q*E + e] and it accumulates D[4q + i][r],
+// i < 4 (batch row 4q + i, output row 16p + r). bf16 tiles: the lane's 16
+// bytes are the B operand of one v_mfma_f32_16x16x32_bf16 (k = t*TK + 8q +
+// 0..7); x[r][those k] enters as three exact bf16 parts (hi, mid, lo: three
+// MFMAs per tile, all products exact), the same D layout.
 //
 // Work split: a wave owns NPW consecutive panels and one chunk of k-tiles; a
 // workgroup's 4 waves take consecutive chunks of the same panels and sum them
@@ -98,13 +101,13 @@ bool launch_tile_weights(hipStream_t s, const void* src, int wtype, int N, int K
 
 BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force, int s_force, int nw) {
   // Measured on MI355X over the GPT-2 decode shapes (2304..50257 rows, K 768..6400,
-  // f32 and bf16): two panels per wave once there are >= 300 panels, one
-  // below; the k range split over 4 workgroups for K >= 150 tiles, over 2 for
+  // f32 and bf16): two panels per wave once there are >= 300 panels (four for
+  // the bf16 LM head), one below; the k range split over 4 workgroups for K >= 150 tiles, over 2 for
   // fewer than 120 panels (too few workgroups otherwise), else not at all.
   BgemvPlan pl{};
   const int TK = wtype == W_F32 ? 16 : 32;
   const int KT = K / TK, NP = (N + 15) / 16;
-  pl.npw = npw_force > 0 ? npw_force : (NP >= 300 ? 2 : 1);
+  pl.npw = npw_force > 0 ? npw_force : (NP >= 1500 && wtype == W_BF16 ? 4 : NP >= 300 ? 2 : 1);
   int S = s_force > 0 ? s_force : (KT >= 150 ? 4 : (NP < 120 ? 2 : 1));
   if (S < 1) S = 1;
   if (S > bgc::SMAX) S = bgc::SMAX;

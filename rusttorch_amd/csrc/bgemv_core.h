@@ -25,6 +25,31 @@ typedef unsigned long long u64;
 constexpr int DEPTH = 4;    // k-tiles in flight per wave
 constexpr int SMAX = 8;     // most workgroups per panel group
 constexpr int LNG_PER = 8;  // statistics groups per lane (ln_groups <= 128)
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// x as the exact sum hi + mid + lo of three bf16 values (each the top 16
+// bits of an f32: hi = x truncated to bf16, mid = (x - hi) truncated, lo =
+// x - hi - mid, whose at most 8 significant bits fit bf16 exactly), packed
+// for the A operand of v_mfma_f32_16x16x32_bf16: dword i of a level holds
+// elements 2i (low half) and 2i + 1.
+__device__ __forceinline__ void split3(const float (&x)[8], u4v& hi, u4v& mid, u4v& lo) {
+  unsigned bh[8], bm[8], bl[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const unsigned xb = __float_as_uint(x[e]);
+    bh[e] = xb & 0xffff0000u;
+    const float r1 = x[e] - __uint_as_float(bh[e]);
+    bm[e] = __float_as_uint(r1) & 0xffff0000u;
+    bl[e] = __float_as_uint(r1 - __uint_as_float(bm[e]));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = __builtin_amdgcn_perm(bh[2 * i + 1], bh[2 * i], 0x07060302u);
+    mid[i] = __builtin_amdgcn_perm(bm[2 * i + 1], bm[2 * i], 0x07060302u);
+    lo[i] = __builtin_amdgcn_perm(bl[2 * i + 1], bl[2 * i], 0x07060302u);
+  }
+}
+__device__ __forceinline__ bf16x8 as_bf16x8(const u4v& v) { return __builtin_bit_cast(bf16x8, v); }
 
 template <bool COH>
 __device__ __forceinline__ float ld1(const float* p) {
@@ -252,13 +277,36 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         if (i0 + d < nt) {
+          if constexpr (WT == W_BF16) {
+            // bf16 weights: the tile is one v_mfma_f32_16x16x32_bf16 B operand;
+            // x enters as three exact bf16 parts, so every product w * part is
+            // exact in f32 and the MFMA accumulates in f32: the f32 GEMV up to
+            // summation order (3 MFMAs per tile instead of 8 of 16x16x4 f32;
+            // measured ~10% faster, with half the error against a float64 sum)
+            float xs[8];
 #pragma unroll
-          for (int e = 0; e < E; ++e) {
-            float xa = x[d][e >> 2][e & 3];
-            if constexpr (LNG) xa *= gv[d][e >> 2][e & 3];
+            for (int e = 0; e < 8; ++e) {
+              xs[e] = x[d][e >> 2][e & 3];
+              if constexpr (LNG) xs[e] *= gv[d][e >> 2][e & 3];
+            }
+            u4v xh, xm, xl;
+            split3(xs, xh, xm, xl);
 #pragma unroll
-            for (int j = 0; j < NPW; ++j)
-              acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, TL::get(w[d][j], e), acc[j], 0, 0, 0);
+            for (int j = 0; j < NPW; ++j) {
+              const bf16x8 wb = as_bf16x8(w[d][j]);
+              acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xh), wb, acc[j], 0, 0, 0);
+              acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xm), wb, acc[j], 0, 0, 0);
+              acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xl), wb, acc[j], 0, 0, 0);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+              float xa = x[d][e >> 2][e & 3];
+              if constexpr (LNG) xa *= gv[d][e >> 2][e & 3];
+#pragma unroll
+              for (int j = 0; j < NPW; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, TL::get(w[d][j], e), acc[j], 0, 0, 0);
+            }
           }
         }
         issue(d, i0 + d + DEPTH);
