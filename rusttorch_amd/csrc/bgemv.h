@@ -42,8 +42,8 @@ struct BgemvArgs {
   // stats_part[g][m] for its panel groups g (plan.groups * 32 floats), with
   // groups of 16 * plan.npw columns.
   float* stats_part;
-  // LM head of the persistent step only: per-row packed argmax keys
-  // (gpt2.rs:858-868), updated with a device-scope atomic max.
+  // LM head: per-row packed argmax keys (gpt2.rs:858-868), updated with a
+  // device-scope atomic max (zero before; the step's finalize resets them).
   unsigned long long* keys;
   float* part;    // workspace of bgemv_work_floats(plan) floats when plan.S > 1
   unsigned* cnt;  // plan.groups zeroed counters when plan.S > 1 (left zeroed)
@@ -68,8 +68,10 @@ BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force = 0, int s_force = 0
 bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a);
 size_t bgemv_work_floats(const BgemvPlan& pl);
 bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a);
-// LayerNorm statistics partials of rows x[r][0, d) as one group of width d:
-// part[r] = (mean, M2) (the ln_part of a following GEMV, ln_groups = 1).
-void launch_row_stats(hipStream_t s, const float* x, int rows, int d, float* part);
+// Decode embedding x[r] = wte[token[r]] + wpe[*pos_dev] of rows r < rows and
+// their LayerNorm statistics partials as one group of width d: part[r] =
+// (mean, M2) (the ln_part of the following GEMV, ln_groups = 1). d <= 2048.
+bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
+                        const int* pos_dev, int rows, int d, float* x, float* part);
 
 }  // namespace rtg

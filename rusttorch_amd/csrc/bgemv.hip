@@ -62,26 +62,53 @@ __global__ __launch_bounds__(64 * BG_NW) void bgemv_kernel(BgemvArgs a) {
   bgc::bgemv_unit<WT, NPW, LNG, BG_NW, false>(a, blockIdx.x, blockIdx.y, red, &last);
 }
 
-__global__ void row_stats_kernel(const float* __restrict__ x, int d, float* __restrict__ part) {
-  // statistics partials of one group of width d per row (two passes as
-  // layer_norm, gpt2.rs:636-666): part[m] = (mean, M2); one wave per row
-  const float* row = x + (size_t)blockIdx.x * d;
-  const int lane = threadIdx.x;
+// Decode embedding of B rows (gpt2.rs:377-384: wte[token] + wpe[position])
+// and the rows' LayerNorm statistics partials as one group of width d
+// (part[m] = (mean, M2), two passes as layer_norm, gpt2.rs:636-666): one
+// workgroup of 256 threads per row.
+__global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict__ wte, int wtype,
+                                                          const float* __restrict__ wpe,
+                                                          const uint32_t* __restrict__ token,
+                                                          const int* __restrict__ pos_dev, int d,
+                                                          float* __restrict__ x, float* __restrict__ part) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const long tok = token[b];
+  const int pos = *pos_dev;
+  float v[8];  // d <= 2048
   float s = 0.f;
-  for (int k = lane; k < d; k += 64) s += row[k];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  const float mean = s / (float)d;
-  float q = 0.f;
-  for (int k = lane; k < d; k += 64) {
-    const float t = row[k] - mean;
-    q += t * t;
+  for (int i = 0; i < 8; ++i) {
+    const int k = tid + 256 * i;
+    v[i] = 0.f;
+    if (k < d) {
+      const float w = wtype == W_F32 ? static_cast<const float*>(wte)[tok * d + k]
+                                     : __uint_as_float((uint32_t)static_cast<const uint16_t*>(wte)[tok * d + k] << 16);
+      v[i] = w + wpe[(long)pos * d + k];
+      x[(long)b * d + k] = v[i];
+      s += v[i];
+    }
   }
+  auto block_sum = [&](float t) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
-  if (lane == 0) {
-    part[2 * blockIdx.x] = mean;
-    part[2 * blockIdx.x + 1] = q;
+    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = t;
+    __syncthreads();
+    const float r = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return r;
+  };
+  const float mean = block_sum(s) / (float)d;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = v[i] - mean;
+    q += tid + 256 * i < d ? t * t : 0.f;
+  }
+  q = block_sum(q);
+  if (tid == 0) {
+    part[2 * b] = mean;
+    part[2 * b + 1] = q;
   }
 }
 
@@ -136,7 +163,7 @@ bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a) {
 size_t bgemv_work_floats(const BgemvPlan& pl) { return pl.S > 1 ? (size_t)pl.groups * pl.S * pl.npw * 256 : 0; }
 
 bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
-  if (!bgemv_args_ok(pl, a) || a.keys) return false;
+  if (!bgemv_args_ok(pl, a)) return false;
   a.S = pl.S;
   a.ktc = pl.ktc;
   const dim3 grid(pl.groups, pl.S);
@@ -159,8 +186,11 @@ bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
   return hipGetLastError() == hipSuccess;
 }
 
-void launch_row_stats(hipStream_t s, const float* x, int rows, int d, float* part) {
-  row_stats_kernel<<<rows, 64, 0, s>>>(x, d, part);
+bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
+                        const int* pos_dev, int rows, int d, float* x, float* part) {
+  if (d > 2048) return false;
+  embed_stats_kernel<<<rows, 256, 0, s>>>(wte, wtype, wpe, token, pos_dev, d, x, part);
+  return hipGetLastError() == hipSuccess;
 }
 
 }  // namespace rtg

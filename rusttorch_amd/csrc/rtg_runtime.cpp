@@ -535,8 +535,8 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
   auto run = [&](const BgemvPlan& pl, const BgemvArgs& a) {
     if (!launch_bgemv(s, pl, a)) throw HipError{"bgemv launch failed"};
   };
-  launch_embed(s, m->wte, m->wtype, m->wpe, c->token_dev, B, 1, 0, c->pos_dev, d, c->x);
-  launch_row_stats(s, c->x, B, d, c->bg_spart);
+  if (!launch_embed_stats(s, m->wte, m->wtype, m->wpe, c->token_dev, c->pos_dev, B, d, c->x, c->bg_spart))
+    throw HipError{"embed_stats launch failed"};
   // shape of the statistics partials the last residual writer left
   int st_groups = 1, st_cols = d;
   auto ln_in = [&](BgemvArgs& a, const float* g, const float* sv) {
@@ -589,6 +589,8 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
     a.C = c->logits; a.ldc = V; a.epi = EPI_BIAS;
     run(bw->pl, a);
   }
+  // (the argmax in the LM head's epilogue, a per-row atomic max per
+  // workgroup, was measured slower than this separate kernel)
   launch_argmax(s, c->logits, V, B, V, c->keys);
 }
 
