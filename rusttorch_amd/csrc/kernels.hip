@@ -1012,11 +1012,11 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
     }
     bm = xor32_max_k(bm);
     const float mn = fmaxf(m, bm);
-    const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+    const float corr = m == -INFINITY ? 0.f : fexp_a(m - mn);
     float ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      s[i] = s[i] == -INFINITY ? 0.f : expf(s[i] - mn);
+      s[i] = s[i] == -INFINITY ? 0.f : fexp_a(s[i] - mn);
       ps += s[i];
     }
     l = l * corr + ps;
