@@ -36,6 +36,10 @@
 namespace rtg {
 namespace pk {
 
+#ifndef PK_PACE
+#define PK_PACE 12
+#endif
+
 constexpr int G = 256;              // workgroups = CUs of an MI355X
 // 8 waves per workgroup = 2 per SIMD, which leaves 256 VGPRs per wave for the
 // two register-resident weight buffers.
@@ -141,6 +145,10 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 template <int D_, int V_, int WT_>
 struct Cfg {
   static constexpr int D = D_, V = V_, WT = WT_, H = D_ / HD, E = WT_ == W_BF16 ? 8 : 4;
+  // refill pacing (seg_issue): measured best at 8 for d = 768 (c1: 4.29k
+  // against 4.21k tokens/s at 12) and at 12 for d = 1024 (c3: 1.54k against
+  // 1.51k at 8); 12 elsewhere
+  static constexpr int PACE = D_ == 768 ? 8 : PK_PACE;
   typedef Geom<3 * D, D, E> GQ;
   typedef Geom<D, D, E> GP;
   typedef Geom<4 * D, D, E> GF;
@@ -318,9 +326,6 @@ struct V16<W_BF16> {
 // [seg_base + cw*SPW, seg_base + (cw+1)*SPW). All bookkeeping is scalar.
 // ---------------------------------------------------------------------------
 
-#ifndef PK_PACE
-#define PK_PACE 12
-#endif
 // PACE > 0: sleep up to PACE*64 clocks between loads while the wave's next
 // input is not ready yet (*ready < next), so a refill does not flood this
 // CU's memory queue ahead of the exchanges; the sleep is cut short (to 128
@@ -450,29 +455,29 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
   seg_issue<WT, MS, GQ, 0>(A, LP[0].wqkv, dz, wg, cw, lane, 0);  // needed first: no pacing
   // each refill is paced until the input of this wave's next compute is ready
   auto rdy = [&](int ph) { return &sm.in_ready[ph]; };
-  seg_issue<WT, MS, GP>(B, LP[0].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), NGLUE);
+  seg_issue<WT, MS, GP, C::PACE>(B, LP[0].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), NGLUE);
   for (int l = 0; l + 1 < p.L; ++l) {
     const unsigned n1 = (unsigned)(l + 1) * NGLUE;
     compute_and_signal(A, sm.in_vec[1], GQ(), PH_QKV, l);   // QKV; refill A with FC
-    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
+    seg_issue<WT, MS, GF, C::PACE>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
     compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);  // attention projection; refill B with MLP projection
-    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
+    seg_issue<WT, MS, GM, C::PACE>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
     compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);    // FC; refill A with next QKV
-    seg_issue<WT, MS, GQ>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
+    seg_issue<WT, MS, GQ, C::PACE>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
     compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);   // MLP projection; refill B with next attention projection
-    seg_issue<WT, MS, GP>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), n1 + NGLUE);
+    seg_issue<WT, MS, GP, C::PACE>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), n1 + NGLUE);
   }
   {  // last layer: the refills after FC / MLP projection are the LM head's chunks 0 and 1
     const int l = p.L - 1;
     const unsigned n1 = (unsigned)(l + 1) * NGLUE;
     compute_and_signal(A, sm.in_vec[1], GQ(), PH_QKV, l);
-    seg_issue<WT, MS, GF>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
+    seg_issue<WT, MS, GF, C::PACE>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
     compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);
-    seg_issue<WT, MS, GM>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
+    seg_issue<WT, MS, GM, C::PACE>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
     compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);
-    seg_issue<WT, MS, GL, PK_PACE, PK_LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
+    seg_issue<WT, MS, GL, C::PACE, PK_LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
     compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);
-    seg_issue<WT, MS, GL, PK_PACE, PK_LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE);
+    seg_issue<WT, MS, GL, C::PACE, PK_LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE);
   }
   // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
   // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
