@@ -149,6 +149,9 @@ struct Cfg {
   // against 4.21k tokens/s at 12) and at 12 for d = 1024 (c3: 1.54k against
   // 1.51k at 8); 12 elsewhere
   static constexpr int PACE = D_ == 768 ? 8 : PK_PACE;
+  // the tied LM head's loads: normal for d = 768 (c1: 4.38k against 4.29k
+  // tokens/s non-temporal), non-temporal otherwise (c3: 1.54k against 1.53k)
+  static constexpr bool LM_NT = D_ != 768;
   typedef Geom<3 * D, D, E> GQ;
   typedef Geom<D, D, E> GP;
   typedef Geom<4 * D, D, E> GF;
@@ -332,9 +335,6 @@ struct V16<W_BF16> {
 // clocks) once the input is ready, after which the remaining loads go out
 // back to back. The pacing is the only conditional part: the loads stay in
 // fixed order.
-#ifndef PK_LM_NT
-#define PK_LM_NT 1
-#endif
 #ifndef PK_W_NT
 #define PK_W_NT 1
 #endif
@@ -475,9 +475,9 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);
     seg_issue<WT, MS, GM, C::PACE>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
     compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);
-    seg_issue<WT, MS, GL, C::PACE, PK_LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
+    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
     compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);
-    seg_issue<WT, MS, GL, C::PACE, PK_LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE);
+    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE);
   }
   // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
   // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
@@ -489,9 +489,9 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
   for (int base = 0; base < segs_here; base += 2 * PER_CHUNK) {
     // nothing else is in flight now: stream at full rate
     seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base);
-    seg_issue<WT, MS, GL, 0, PK_LM_NT>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
+    seg_issue<WT, MS, GL, 0, C::LM_NT>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
     seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK);
-    seg_issue<WT, MS, GL, 0, PK_LM_NT>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
+    seg_issue<WT, MS, GL, 0, C::LM_NT>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
   }
   lds_release();
   if (lane == 0) lds_add(&sm.gemv_done, 1);
