@@ -423,6 +423,21 @@ def test_persistent_batched_step_matches_oracle(O, monkeypatch):
     assert out.tolist() == ref.tolist()
 
 
+def test_batched_step_odd_batch_and_batch_one(O, monkeypatch):
+    """The tile-ordered batched step with partly used MFMA rows: 13 sequences
+    (logits against the oracle), and batch 1 with the persistent kernel
+    switched off (RTG_DISABLE_PERSISTENT=1: the graph path with one row),
+    greedy ids against the oracle."""
+    sd, sh, m = gpu_model("small")
+    _batched_step_logits(O, sd, sh, m, 13, 6, 2, 500, "small b=13")
+    monkeypatch.setenv("RTG_DISABLE_PERSISTENT", "1")
+    m1 = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    prompt = synth.make_tokens(12, sh.vocab_size, stream=520)
+    assert m1.generate_cached(prompt, 16, 0.0) == om.generate_cached(prompt, 16)
+    m1.close()
+
+
 def test_long_prefill_attention_blocks(O):
     """Prefill attention over many key blocks, several query blocks, a past
     length that is not a block multiple and a second chunk appended to a
