@@ -568,6 +568,20 @@ def test_bf16_batched_decode_matches_single():
         assert out[b].tolist() == m.generate_cached(prompts[b], 20, 0.0)
 
 
+def test_batch_above_16_per_op_fallback(O):
+    """More than 16 sequences fall back to the per-op decode kernels (the
+    32-row skinny MFMA GEMM, LayerNorm and the attention kernel): 20
+    sequences of the mini model, ids against single runs and the oracle."""
+    sd, sh, m = gpu_model("mini")
+    B = 20
+    prompts = np.stack([synth.make_tokens(6, sh.vocab_size, stream=530 + b) for b in range(B)])
+    out = m.generate_cached_batched(prompts, 10)
+    om = O.OracleModel.from_shape(sd, sh)
+    for b in (0, 7, 19):
+        assert out[b].tolist() == m.generate_cached(prompts[b], 10, 0.0)
+        assert out[b].tolist() == om.generate_cached(prompts[b], 10)
+
+
 def test_bf16_storage_matches_oracle(O):
     sh = synth.SHAPES["mini"]
     sd = synth.make_weights(sh, bf16=True)
