@@ -142,7 +142,7 @@ def run_prefill(a):
         "data": "synthetic: seeded N(0,0.02) random-init weights, uniform random token ids",
         "config": {"workload": f"{a.workload}: GPT-2 {shape_name}, batch {B}, prefill {T} tokens, full logits",
                    "batch": B, "tokens": T, "weights": "f32"},
-        "roofline": {"bound": "mfma", "kernel": "whole prefill (gemm_kernel dominant)",
+        "roofline": {"bound": "mfma", "kernel": "whole prefill (gemm_lds_kernel dominant)",
                      "achieved": round(achieved, 2), "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), "flops_per_step": flops,
                      "traffic": None},

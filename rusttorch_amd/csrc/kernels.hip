@@ -8,6 +8,7 @@
 // nn/safetensors.rs:389-391).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "attn_core.h"
 #include "kernels.h"
@@ -588,6 +589,177 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
   }
 }
 
+// Prefill GEMM for f32 weights, K % 64 == 0: the same 128x128 tile and MFMA
+// arrangement, fed by LDS-direct loads (global_load_lds_dwordx4) through a
+// GL_NS-stage LDS ring, so no registers hold tiles in flight and three k-tiles
+// are in flight while one is computed.
+// - A stage holds the A and W tiles as 8 + 8 groups of 16 rows x 16 k (1 KiB,
+//   one load instruction each: lane i fills bytes [16i, 16i + 16) of its
+//   group). Lane i loads row r = i / 4 of the group, 4-float chunk
+//   c = (i % 4) ^ gl_swz(row): an XOR swizzle that makes the operand reads
+//   below conflict-free.
+// - k is permuted inside a tile: MFMA step s of lane half h (lane / 32) uses
+//   k = 8h + s, so a lane reads its 8 values of a row with two ds_read_b128.
+//   A and W use the same permutation, so the products are those of the plain
+//   order (the sum is taken over all 16 k of the tile either way).
+constexpr int GL_NS = 4;
+__device__ __forceinline__ int gl_swz(int row) { return (row >> 2) & 3; }
+
+// global_load_lds_dwordx4 written out, so that the compiler's wait-count pass
+// does not tie later LDS reads to these loads (it waited for all of them
+// before every fourth tile's reads); the kernel orders them itself with
+// gl_wait_barrier. M0 carries the wave-uniform LDS address.
+__device__ __forceinline__ void gl_dma16(const float* src, const float* lds_dst) {
+  const unsigned m0v =
+      __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const __attribute__((address_space(3))) float*)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v) : "memory", "m0");
+}
+// Wait until at most N of this wave's vector memory operations are
+// outstanding, then a workgroup barrier; memory accesses do not move across.
+template <int N>
+__device__ __forceinline__ void gl_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// One k-tile step of gemm_lds_kernel on stage ST (a separate LDS array per
+// stage, so the compiler's wait-count pass can tell which outstanding
+// LDS-direct loads a read depends on).
+template <int ST>
+__device__ __forceinline__ void gl_step(int kt, int nk, float (&lds)[2][GBM * 16], float (&nxt)[2][GBM * 16],
+                                        const float* const (&asrc)[2], const float* const (&wsrc)[2], int wave,
+                                        const int (&aoff)[2][2], const int (&woff)[2][2], floatx16 (&acc)[2][2]) {
+  // tile kt has landed once at most the loads of the GL_NS - 2 later tiles
+  // (4 instructions each) are still outstanding; after the barrier every
+  // wave's loads of tile kt are in and no wave reads tile kt - 1 any more
+  if (kt + GL_NS - 2 < nk) gl_wait_barrier<(GL_NS - 2) * 4>();
+  else gl_wait_barrier<0>();
+  if (kt + GL_NS - 1 < nk) {
+    const int k = (kt + GL_NS - 1) * 16;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int g = 2 * wave + q;
+      gl_dma16(asrc[q] + k, &nxt[0][g * 256]);
+      gl_dma16(wsrc[q] + k, &nxt[1][g * 256]);
+    }
+  }
+  float4 a[2][2], b[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      a[i][c] = *reinterpret_cast<const float4*>(&lds[0][aoff[i][c]]);
+      b[i][c] = *reinterpret_cast<const float4*>(&lds[1][woff[i][c]]);
+    }
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float4& av = a[i][s >> 2];
+        const float4& bv = b[j][s >> 2];
+        const int e = s & 3;
+        const float x = e == 0 ? av.x : e == 1 ? av.y : e == 2 ? av.z : av.w;
+        const float y = e == 0 ? bv.x : e == 1 ? bv.y : e == 2 ? bv.z : bv.w;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i][j], 0, 0, 0);
+      }
+  }
+}
+
+__global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__ A, int lda,
+                                                       const float* __restrict__ W, const float* __restrict__ bias,
+                                                       float* __restrict__ C, long ldc, int M, int N, int K, int epi,
+                                                       int m_fast) {
+  __shared__ __attribute__((aligned(16))) float st0[2][GBM * 16];
+  __shared__ __attribute__((aligned(16))) float st1[2][GBM * 16];
+  __shared__ __attribute__((aligned(16))) float st2[2][GBM * 16];
+  __shared__ __attribute__((aligned(16))) float st3[2][GBM * 16];
+  static_assert(GL_NS == 4, "four stage arrays");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  // block order: with m_fast the row blocks of one W column block are
+  // consecutive (W read once while A cycles through the cache), else the
+  // column blocks of one A row block (A read once while W cycles)
+  const int nmb = (M + GBM - 1) / GBM, nnb = (N + GBN - 1) / GBN;
+  const int bid = blockIdx.x;
+  const int m0 = (m_fast ? bid % nmb : bid / nnb) * GBM, n0 = (m_fast ? bid / nmb : bid % nnb) * GBN;
+
+  // this lane's load sources: groups 2*wave and 2*wave + 1 of A and of W
+  const int lr = lane >> 2;
+  const float* asrc[2];
+  const float* wsrc[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = (2 * wave + q) * 16 + lr;
+    const int c = (lane & 3) ^ gl_swz(row);
+    asrc[q] = A + (size_t)min(m0 + row, M - 1) * lda + c * 4;
+    wsrc[q] = W + (size_t)min(n0 + row, N - 1) * K + c * 4;
+  }
+  auto issue = [&](int kt, float (&st)[2][GBM * 16]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int g = 2 * wave + q;
+      gl_dma16(asrc[q] + kt * 16, &st[0][g * 256]);
+      gl_dma16(wsrc[q] + kt * 16, &st[1][g * 256]);
+    }
+  };
+
+  // operand read offsets (floats within a stage's A or W tile): rows
+  // wm + 32i + lane % 32 (A) and wn + 32j + lane % 32 (W), chunks 2h, 2h + 1
+  const int h = lane >> 5;
+  int aoff[2][2], woff[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ra = wm + 32 * i + (lane & 31), rw = wn + 32 * i + (lane & 31);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      aoff[i][c] = ra * 16 + (((2 * h + c) ^ gl_swz(ra)) * 4);
+      woff[i][c] = rw * 16 + (((2 * h + c) ^ gl_swz(rw)) * 4);
+    }
+  }
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int nk = K / 16;  // a multiple of GL_NS (K % 64 == 0)
+  issue(0, st0);
+  issue(1, st1);
+  issue(2, st2);
+  for (int kt = 0; kt < nk; kt += GL_NS) {
+    gl_step<0>(kt, nk, st0, st3, asrc, wsrc, wave, aoff, woff, acc);
+    gl_step<1>(kt + 1, nk, st1, st0, asrc, wsrc, wave, aoff, woff, acc);
+    gl_step<2>(kt + 2, nk, st2, st1, asrc, wsrc, wave, aoff, woff, acc);
+    gl_step<3>(kt + 3, nk, st3, st2, asrc, wsrc, wave, aoff, woff, acc);
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn + j * 32 + (lane & 31);
+      if (n >= N) continue;
+      const float bv = bias ? bias[n] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (m < M) {
+          float* cp = C + (size_t)m * ldc + n;
+          const float v = acc[i][j][e];
+          if (epi == EPI_BIAS) *cp = v + bv;
+          else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
+          else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
+          else *cp = v;
+        }
+      }
+    }
+  }
+}
+
 // Skinny GEMM for few rows (a short prompt): the 128x128 tile kernel would
 // launch only N/128 workgroups. Here a workgroup computes a 32x32 output tile
 // and each of its 4 waves a quarter of K. Step e of a wave's MFMA chain pairs
@@ -791,11 +963,21 @@ static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W,
   return true;
 }
 
+// RTG_GEMM_REG=1 keeps f32 weights on the register-staged gemm_kernel (for A/B timing).
+static bool gemm_reg_forced() {
+  static const bool v = getenv("RTG_GEMM_REG") != nullptr;
+  return v;
+}
+
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
                  long ldc, int M, int N, int K, int epi) {
   if (launch_skinny(s, A, lda, W, wtype, bias, C, ldc, M, N, K, epi, SkinnyQkv{})) return;
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
-  if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
+  if (wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(W) & 15) == 0 && !gemm_reg_forced())
+    gemm_lds_kernel<<<grid.x * grid.y, 256, 0, s>>>(A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N,
+                                                    K, epi, N > M ? 1 : 0);
+  else if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
   else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
 }
 
