@@ -975,6 +975,10 @@ void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtyp
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
   if (wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(W) & 15) == 0 && !gemm_reg_forced())
+    // (256 x 128 tiles with 3 stages, bounded to two waves per SIMD, were 2-4%
+    // faster on the c4 shapes without an epilogue but made the c4 prefill
+    // slower, 70.7k against 72.5k tokens/s; 3 stages at three waves per SIMD
+    // and 2 stages at four were no faster than this kernel)
     gemm_lds_kernel<<<grid.x * grid.y, 256, 0, s>>>(A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N,
                                                     K, epi, N > M ? 1 : 0);
   else if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
