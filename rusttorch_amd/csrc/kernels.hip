@@ -124,9 +124,62 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     out[(size_t)blockIdx.x * d + j] = (row[j] - mean) * inv_std * w[j] + b[j];
 }
 
+// The same two-pass LayerNorm with one wave per row (4 rows per workgroup)
+// for d % 4 == 0, d <= 2048: the row stays in registers (lane l holds the
+// 16-byte chunks l, l + 64, ...), sums are wave reductions (DPP row sums, then
+// the lane-16 / lane-32 swaps), no LDS and no barriers. The block-per-row
+// kernel above needed three passes and two workgroup reductions per row
+// (142 us for c4's 32768 x 1280, 2.4 TB/s).
+constexpr int LNW_MAXC = 8;  // 16-byte chunks per lane: d <= 64 * 4 * 8
+// full-wave sum in every lane on DPP and permlane swaps (no LDS traffic)
+__device__ __forceinline__ float wave_sum_dpp(float v) { return xor32_sum_k(xor16_sum_k(row16_sum_k(v))); }
+
+__global__ __launch_bounds__(256) void layernorm_wave_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                             const float* __restrict__ b, float eps, int rows, int d,
+                                                             float* __restrict__ out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;  // wave-uniform
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * d);
+  const int nc = d >> 2;
+  float4 v[LNW_MAXC];
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < LNW_MAXC; ++u) {
+    const int ch = lane + 64 * u;
+    v[u] = ch < nc ? xr[ch] : make_float4(0.f, 0.f, 0.f, 0.f);
+    sum += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+  }
+  const float mean = wave_sum_dpp(sum) / (float)d;
+  float sq = 0.f;
+#pragma unroll
+  for (int u = 0; u < LNW_MAXC; ++u) {
+    if (lane + 64 * u < nc) {
+      const float a = v[u].x - mean, bb = v[u].y - mean, cc = v[u].z - mean, dd = v[u].w - mean;
+      sq += (a * a + bb * bb) + (cc * cc + dd * dd);
+    }
+  }
+  const float var = wave_sum_dpp(sq) / (float)d;
+  const float inv_std = 1.0f / sqrtf(var + eps);
+  float4* orow = reinterpret_cast<float4*>(out + (size_t)row * d);
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  const float4* b4 = reinterpret_cast<const float4*>(b);
+#pragma unroll
+  for (int u = 0; u < LNW_MAXC; ++u) {
+    const int ch = lane + 64 * u;
+    if (ch < nc) {
+      const float4 g = w4[ch], bi = b4[ch];
+      orow[ch] = make_float4((v[u].x - mean) * inv_std * g.x + bi.x, (v[u].y - mean) * inv_std * g.y + bi.y,
+                             (v[u].z - mean) * inv_std * g.z + bi.z, (v[u].w - mean) * inv_std * g.w + bi.w);
+    }
+  }
+}
+
 void launch_layernorm(hipStream_t s, const float* x, const float* w, const float* b, float eps, int rows, int d,
                       float* out) {
-  layernorm_kernel<<<rows, 256, 0, s>>>(x, w, b, eps, d, out);
+  if (d % 4 == 0 && d <= 256 * LNW_MAXC)
+    layernorm_wave_kernel<<<(rows + 3) / 4, 256, 0, s>>>(x, w, b, eps, rows, d, out);
+  else
+    layernorm_kernel<<<rows, 256, 0, s>>>(x, w, b, eps, d, out);
 }
 
 // ---------------------------------------------------------------------------
