@@ -67,6 +67,13 @@ void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtyp
                  long ldc, int M, int N, int K, int epi);
 // Prefill: append k/v columns of qkv [S*T][3d] into the cache at past.. past+T.
 void launch_kv_append(hipStream_t s, const float* qkv, int S, int T, int past, KvDst kv);
+// Prefill c_attn: C = A W^T + bias with the k/v columns ([d, 3d)) of row
+// s*T + t written into the cache at position past + t instead of C (the
+// append of LayerKVCache::append, gpt2.rs:500-514, in the GEMM's epilogue).
+// Falls back to launch_gemm + launch_kv_append where the fused kernel does not
+// apply (f32 weights, K % 64 == 0, 16-byte aligned operands, more than 64 rows).
+void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
+                     long ldc, int M, int K, int S, int T, int past, KvDst kv);
 // Prefill causal attention for S sequences of T new tokens at offset past.
 void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past, const float* kc, const float* vc,
                          int n_head, int n_pos, int d, float* out);

@@ -722,7 +722,7 @@ __device__ __forceinline__ void gl_step(int kt, int nk, float (&lds)[2][GBM * 16
 __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__ A, int lda,
                                                        const float* __restrict__ W, const float* __restrict__ bias,
                                                        float* __restrict__ C, long ldc, int M, int N, int K, int epi,
-                                                       int m_fast) {
+                                                       int m_fast, KvDst kv, int kv_T, int kv_past) {
   __shared__ __attribute__((aligned(16))) float st0[2][GBM * 16];
   __shared__ __attribute__((aligned(16))) float st1[2][GBM * 16];
   __shared__ __attribute__((aligned(16))) float st2[2][GBM * 16];
@@ -797,6 +797,20 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__
       const int n = n0 + wn + j * 32 + (lane & 31);
       if (n >= N) continue;
       const float bv = bias ? bias[n] : 0.f;
+      if (kv.k != nullptr && n >= kv.d) {
+        // k / v column of c_attn: into the cache at (sequence, head, past + t)
+        const int which = n >= 2 * kv.d, cc = n - kv.d - which * kv.d;
+        float* base = (which ? kv.v : kv.k) + (size_t)(cc >> 6) * kv.n_pos * 64 + (cc & 63);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (m < M) {
+            const int sq = m / kv_T, t = m - sq * kv_T;
+            base[((size_t)sq * kv.n_head * kv.n_pos + kv_past + t) * 64] = acc[i][j][e] + bv;
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
@@ -1033,9 +1047,23 @@ void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtyp
     // slower, 70.7k against 72.5k tokens/s; 3 stages at three waves per SIMD
     // and 2 stages at four were no faster than this kernel)
     gemm_lds_kernel<<<grid.x * grid.y, 256, 0, s>>>(A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N,
-                                                    K, epi, N > M ? 1 : 0);
+                                                    K, epi, N > M ? 1 : 0, KvDst{}, 1, 0);
   else if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
   else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
+}
+
+void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
+                     long ldc, int M, int K, int S, int T, int past, KvDst kv) {
+  const int N = 3 * kv.d;
+  if (M > 64 && wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(W) & 15) == 0 && kv.d == 64 * kv.n_head && !gemm_reg_forced()) {
+    const int nb = ((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM);
+    gemm_lds_kernel<<<nb, 256, 0, s>>>(A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, EPI_BIAS,
+                                       N > M ? 1 : 0, kv, T, past);
+    return;
+  }
+  launch_gemm(s, A, lda, W, wtype, bias, C, ldc, M, N, K, EPI_BIAS);
+  launch_kv_append(s, C, S, T, past, kv);
 }
 
 // ---------------------------------------------------------------------------

@@ -270,8 +270,7 @@ static void enqueue_prefill(rtg_cache* c, const uint32_t* ids_dev, size_t S, siz
     const LayerW& L = m->layers[l];
     KvDst kv = kv_layer(c, l);
     launch_layernorm(s, c->x, L.ln1w, L.ln1b, eps, M, d, c->ln);
-    launch_gemm(s, c->ln, d, L.wqkv, m->wtype, L.bqkv, c->qkv, 3 * d, M, 3 * d, d, EPI_BIAS);
-    launch_kv_append(s, c->qkv, (int)S, (int)T, (int)past, kv);
+    launch_gemm_qkv(s, c->ln, d, L.wqkv, m->wtype, L.bqkv, c->qkv, 3 * d, M, d, (int)S, (int)T, (int)past, kv);
     launch_attn_prefill(s, c->qkv, (int)S, (int)T, (int)past, kv.k, kv.v, kv.n_head, kv.n_pos, d, c->att);
     launch_gemm(s, c->att, d, L.waproj, m->wtype, L.baproj, c->x, d, M, d, d, EPI_BIAS_RESID);
     launch_layernorm(s, c->x, L.ln2w, L.ln2b, eps, M, d, c->ln);
