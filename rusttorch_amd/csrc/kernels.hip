@@ -1198,8 +1198,11 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
     int H, int P, int d, int nqb, float* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) float Ks[FA_K][FA_KP];
   __shared__ __attribute__((aligned(16))) float Vt[64][FA_VP];
-  const int qb = nqb - 1 - (int)blockIdx.x;  // the longest (last) query blocks first
-  const int h = blockIdx.y, sidx = blockIdx.z;
+  // the query block is the slowest grid dimension, longest (last) blocks
+  // first: every (sequence, head)'s longest block is dispatched before any
+  // shorter one, which keeps the tail of the grid short
+  const int qb = nqb - 1 - (int)blockIdx.z;
+  const int h = blockIdx.x, sidx = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane & 31, hh = lane >> 5;
   const int qi = qb * FA_QW * FA_W + wave * FA_QW + c;  // this lane's query (0..T-1 when valid)
@@ -1326,7 +1329,7 @@ void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past
                          int n_head, int n_pos, int d, float* out) {
   if (d / n_head == 64) {
     const int nqb = (T + FA_QW * FA_W - 1) / (FA_QW * FA_W);
-    dim3 grid(nqb, n_head, S);
+    dim3 grid(n_head, S, nqb);
     attn_prefill_mfma_kernel<<<grid, FA_QW * 2 * FA_W, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
     return;
   }
