@@ -33,6 +33,7 @@ struct orc_model {
   const float *wte, *wpe, *ln_f_w, *ln_f_b;
   struct orc_layer* layers;
   int threads;
+  int lm_direct; /* lm_head without the materialised transpose (same values) */
 };
 
 /* KVCache / LayerKVCache (gpt2.rs:111-175): keys[layer][head] hold
@@ -80,33 +81,59 @@ void orc_layer_norm(const float* x, size_t rows, size_t n, const float* w, const
 }
 
 /* matrix::matmul (ops/matrix.rs:36-117) for 2D f32: out[m,n] = a[m,k] @ b[k,n].
- * Each output element is summed over k in ascending order starting from 0.
- * Blocked over columns for cache reuse; the per-element order does not depend
- * on the blocking or on the thread count. */
-void orc_matmul(const float* a, size_t m, size_t k, const float* b, size_t n, float* out, int threads) {
-  const size_t NB = 256;
-  long nblocks = (long)((n + NB - 1) / NB);
-  (void)threads;
-#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1) if (threads > 1)
-  for (long nbk = 0; nbk < nblocks; ++nbk) {
-    size_t n0 = (size_t)nbk * NB;
-    size_t n1 = n0 + NB < n ? n0 + NB : n;
-    for (size_t i = 0; i < m; ++i) {
-      float* o = out + i * n;
-      for (size_t j = n0; j < n1; ++j) o[j] = 0.0f;
-    }
-    for (size_t i0 = 0; i0 < m; i0 += 8) {
-      size_t i1 = i0 + 8 < m ? i0 + 8 : m;
-      for (size_t kk = 0; kk < k; ++kk) {
-        const float* brow = b + kk * n;
-        for (size_t i = i0; i < i1; ++i) {
-          float av = a[i * k + kk];
-          float* o = out + i * n;
-          for (size_t j = n0; j < n1; ++j) o[j] += av * brow[j];
-        }
+ * Each output element starts from 0.0f and adds a[i][kk] * b[kk][j] for kk in
+ * ascending order (one rounded product, one rounded add per term). The tiles
+ * below only decide which elements are accumulated together (in registers,
+ * MI x NJ at a time); no element's order depends on the tiling or on the
+ * thread count. */
+enum { MI = 4, NJ = 32, MROWS = 64 };
+
+/* rows [i0, i0 + ni) (ni <= MI) x columns [j0, j0 + NJ) */
+static void mm_tile(const float* a, size_t k, const float* b, size_t n, float* out, size_t i0, size_t ni, size_t j0) {
+  float acc[MI][NJ];
+  memset(acc, 0, sizeof acc);
+  if (ni == MI) {
+    for (size_t kk = 0; kk < k; ++kk) {
+      const float* br = b + kk * n + j0;
+      const float a0 = a[(i0 + 0) * k + kk], a1 = a[(i0 + 1) * k + kk];
+      const float a2 = a[(i0 + 2) * k + kk], a3 = a[(i0 + 3) * k + kk];
+      for (int j = 0; j < NJ; ++j) {
+        acc[0][j] += a0 * br[j];
+        acc[1][j] += a1 * br[j];
+        acc[2][j] += a2 * br[j];
+        acc[3][j] += a3 * br[j];
       }
     }
+  } else {
+    for (size_t ii = 0; ii < ni; ++ii)
+      for (size_t kk = 0; kk < k; ++kk) {
+        const float* br = b + kk * n + j0;
+        const float av = a[(i0 + ii) * k + kk];
+        for (int j = 0; j < NJ; ++j) acc[ii][j] += av * br[j];
+      }
   }
+  for (size_t ii = 0; ii < ni; ++ii) memcpy(out + (i0 + ii) * n + j0, acc[ii], NJ * sizeof(float));
+}
+
+void orc_matmul(const float* a, size_t m, size_t k, const float* b, size_t n, float* out, int threads) {
+  const long njb = (long)(n / NJ), nmb = (long)((m + MROWS - 1) / MROWS);
+  (void)threads;
+  /* full column blocks: work items (row group, column block) */
+#pragma omp parallel for schedule(dynamic, 4) num_threads(threads > 0 ? threads : 1) if (threads > 1)
+  for (long w = 0; w < njb * nmb; ++w) {
+    const size_t j0 = (size_t)(w % njb) * NJ, r0 = (size_t)(w / njb) * MROWS;
+    const size_t r1 = r0 + MROWS < m ? r0 + MROWS : m;
+    for (size_t i0 = r0; i0 < r1; i0 += MI) mm_tile(a, k, b, n, out, i0, r1 - i0 < MI ? r1 - i0 : MI, j0);
+  }
+  /* the last n % NJ columns */
+  const size_t jt = (size_t)njb * NJ;
+  if (jt < n)
+    for (size_t i = 0; i < m; ++i)
+      for (size_t j = jt; j < n; ++j) {
+        float acc = 0.0f;
+        for (size_t kk = 0; kk < k; ++kk) acc += a[i * k + kk] * b[kk * n + j];
+        out[i * n + j] = acc;
+      }
 }
 
 /* conv1d_forward, gpt2.rs:628-633: y = x @ W + b, W is [in, out]; the bias
@@ -324,6 +351,8 @@ void orc_model_destroy(orc_model* m) {
 
 void orc_model_set_threads(orc_model* m, int threads) { m->threads = threads > 0 ? threads : 1; }
 
+void orc_model_set_lm_direct(orc_model* m, int on) { m->lm_direct = on != 0; }
+
 /* num_parameters, gpt2.rs:541-563. */
 size_t orc_num_parameters(const orc_model* m) {
   size_t d = m->cfg.n_embd, f = 4 * d;
@@ -370,16 +399,25 @@ int orc_cache_read(const orc_cache* c, size_t layer, size_t head, int values, fl
   return 0;
 }
 
-/* multi_head_attention_cached, gpt2.rs:772-834 over this layer's cache. */
+/* multi_head_attention_cached, gpt2.rs:772-834 over this layer's cache.
+ * Every (head, row) pair is independent; with threads > 1 they are spread
+ * over threads, each computing its pairs exactly as the single-threaded loop
+ * does (scores in j order, softmax_inplace, then each output dim summed over
+ * j in ascending order). */
 static void attention_cached(const orc_cache* c, size_t layer, const float* q, size_t new_len, size_t past_len,
-                             float* out) {
+                             float* out, int threads) {
   size_t hd = c->head_dim, nh = c->n_head, n_embd = nh * hd;
   float scale = 1.0f / sqrtf((float)hd);
-  float* scores = (float*)malloc((past_len + new_len) * sizeof(float));
-  for (size_t h = 0; h < nh; ++h) {
-    const float* K = kv_ptr(c, c->keys, layer, h);
-    const float* V = kv_ptr(c, c->values, layer, h);
-    for (size_t i = 0; i < new_len; ++i) {
+  const long rows = (long)(nh * new_len);
+#pragma omp parallel num_threads(threads > 0 ? threads : 1) if (threads > 1 && rows > 1)
+  {
+    float* scores = (float*)malloc((past_len + new_len) * sizeof(float));
+    float* val = (float*)malloc(hd * sizeof(float));
+#pragma omp for schedule(dynamic, 1)
+    for (long r = 0; r < rows; ++r) {
+      const size_t h = (size_t)r / new_len, i = new_len - 1 - (size_t)r % new_len; /* longest rows first */
+      const float* K = kv_ptr(c, c->keys, layer, h);
+      const float* V = kv_ptr(c, c->values, layer, h);
       size_t attend = past_len + i + 1;
       const float* qi = q + i * n_embd + h * hd;
       for (size_t j = 0; j < attend; ++j) {
@@ -388,14 +426,16 @@ static void attention_cached(const orc_cache* c, size_t layer, const float* q, s
         scores[j] = dot * scale;
       }
       softmax_inplace(scores, attend);
-      for (size_t d = 0; d < hd; ++d) {
-        float val = 0.0f;
-        for (size_t j = 0; j < attend; ++j) val += scores[j] * V[j * hd + d];
-        out[i * n_embd + h * hd + d] = val;
+      for (size_t d = 0; d < hd; ++d) val[d] = 0.0f;
+      for (size_t j = 0; j < attend; ++j) {
+        const float sj = scores[j];
+        for (size_t d = 0; d < hd; ++d) val[d] += sj * V[j * hd + d];
       }
+      for (size_t d = 0; d < hd; ++d) out[i * n_embd + h * hd + d] = val[d];
     }
+    free(val);
+    free(scores);
   }
-  free(scores);
 }
 
 static void vec_add(const float* a, const float* b, float* out, size_t n) {
@@ -419,7 +459,10 @@ static void run_layer(const orc_model* m, size_t li, float* x, size_t T, orc_cac
   float* fc = (float*)malloc(T * f * sizeof(float));
   float* act = (float*)malloc(T * f * sizeof(float));
 
-  orc_layer_norm(x, T, d, L->ln_1_w, L->ln_1_b, eps, ln);
+  /* row-wise ops (LayerNorm, gelu_new) split over rows when threaded: each
+   * row is computed exactly as the single-threaded call computes it */
+#pragma omp parallel for num_threads(th) if (th > 1 && T > 1)
+  for (long i = 0; i < (long)T; ++i) orc_layer_norm(x + i * d, 1, d, L->ln_1_w, L->ln_1_b, eps, ln + i * d);
   orc_conv1d(ln, T, d, L->c_attn_w, L->c_attn_b, 3 * d, qkv, th);
   orc_slice_columns(qkv, T, 3 * d, 0, d, q);
   orc_slice_columns(qkv, T, 3 * d, d, 2 * d, k);
@@ -433,15 +476,17 @@ static void run_layer(const orc_model* m, size_t li, float* x, size_t T, orc_cac
                hd * sizeof(float));
       }
     cache->cached_len[li] += T;
-    attention_cached(cache, li, q, T, past_len, att);
+    attention_cached(cache, li, q, T, past_len, att, th);
   } else {
     orc_multi_head_attention(q, k, v, nh, hd, T, att);
   }
   orc_conv1d(att, T, d, L->c_proj_w, L->c_proj_b, d, proj, th);
   vec_add(x, proj, x, T * d); /* x2 = x + attn_proj */
-  orc_layer_norm(x, T, d, L->ln_2_w, L->ln_2_b, eps, ln);
+#pragma omp parallel for num_threads(th) if (th > 1 && T > 1)
+  for (long i = 0; i < (long)T; ++i) orc_layer_norm(x + i * d, 1, d, L->ln_2_w, L->ln_2_b, eps, ln + i * d);
   orc_conv1d(ln, T, d, L->fc_w, L->fc_b, f, fc, th);
-  orc_gelu_new(fc, T * f, act);
+#pragma omp parallel for num_threads(th) if (th > 1 && T > 1)
+  for (long i = 0; i < (long)T; ++i) orc_gelu_new(fc + i * f, f, act + i * f);
   orc_conv1d(act, T, f, L->mproj_w, L->mproj_b, d, proj, th);
   vec_add(x, proj, x, T * d); /* x2 + proj */
 
@@ -449,14 +494,35 @@ static void run_layer(const orc_model* m, size_t li, float* x, size_t T, orc_cac
 }
 
 /* Shared tail: ln_f then the tied LM head x @ wte^T (gpt2.rs:392-396). The
- * transpose is materialised exactly as matrix::transpose does. */
+ * transpose is materialised as matrix::transpose does (the reference's cost
+ * per call), unless lm_direct is set: then each logit is summed straight from
+ * the contiguous wte row, over j in ascending order from 0.0f, which is the
+ * same arithmetic as the matmul over the transposed copy (bit-identical). */
 static void lm_head(const orc_model* m, const float* x, size_t T, float* logits) {
   size_t d = m->cfg.n_embd, V = m->cfg.vocab_size;
   float* ln = (float*)malloc(T * d * sizeof(float));
   orc_layer_norm(x, T, d, m->ln_f_w, m->ln_f_b, m->cfg.layer_norm_epsilon, ln);
+  if (m->lm_direct && T <= 8) { /* (many rows: the tiled matmul is faster) */
+#pragma omp parallel for schedule(static) num_threads(m->threads > 0 ? m->threads : 1) if (m->threads > 1)
+    for (long v = 0; v < (long)V; ++v) {
+      const float* w = m->wte + (size_t)v * d;
+      for (size_t i = 0; i < T; ++i) {
+        float acc = 0.0f;
+        for (size_t j = 0; j < d; ++j) acc += ln[i * d + j] * w[j];
+        logits[i * V + (size_t)v] = acc;
+      }
+    }
+    free(ln);
+    return;
+  }
   float* wt = (float*)malloc(d * V * sizeof(float));
-  for (size_t v = 0; v < V; ++v)
-    for (size_t j = 0; j < d; ++j) wt[j * V + v] = m->wte[v * d + j];
+  /* the same copy, in 64 x 64 blocks so that reads and writes stay in cache */
+  const long nvb = (long)((V + 63) / 64);
+#pragma omp parallel for schedule(static) num_threads(m->threads > 0 ? m->threads : 1) if (m->threads > 1)
+  for (long vb = 0; vb < nvb; ++vb)
+    for (size_t j0 = 0; j0 < d; j0 += 64)
+      for (size_t v = (size_t)vb * 64; v < V && v < (size_t)vb * 64 + 64; ++v)
+        for (size_t j = j0; j < d && j < j0 + 64; ++j) wt[j * V + v] = m->wte[v * d + j];
   orc_matmul(ln, T, d, wt, V, logits, m->threads);
   free(wt);
   free(ln);

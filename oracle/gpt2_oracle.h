@@ -51,6 +51,10 @@ int orc_model_create(const orc_config* cfg, const char* const* names, const floa
                      orc_model** out, char* err);
 void orc_model_destroy(orc_model* m);
 void orc_model_set_threads(orc_model* m, int threads);
+/* on != 0: the tied LM head sums each logit from its wte row instead of
+ * multiplying by a materialised transpose (the reference's per-call copy,
+ * gpt2.rs:395). Same arithmetic per logit, so the same values; faster. */
+void orc_model_set_lm_direct(orc_model* m, int on);
 size_t orc_num_parameters(const orc_model* m);
 
 orc_cache* orc_cache_new(const orc_model* m);

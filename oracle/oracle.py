@@ -61,6 +61,7 @@ def lib() -> C.CDLL:
                                        C.POINTER(vp), C.c_char_p]
         L.orc_model_destroy.argtypes = [vp]
         L.orc_model_set_threads.argtypes = [vp, C.c_int]
+        L.orc_model_set_lm_direct.argtypes = [vp, C.c_int]
         L.orc_num_parameters.argtypes = [vp]
         L.orc_num_parameters.restype = sz
         L.orc_cache_new.argtypes = [vp]
@@ -204,7 +205,12 @@ class OracleCache:
 class OracleModel:
     """Gpt2Model::from_state_dict over borrowed float32 arrays."""
 
-    def __init__(self, sd: dict, vocab_size, n_positions, n_embd, n_layer, n_head, eps=1e-5, threads=1):
+    def __init__(self, sd: dict, vocab_size, n_positions, n_embd, n_layer, n_head, eps=1e-5, threads=1,
+                 lm_direct=True):
+        """lm_direct: the tied LM head sums each logit from its wte row
+        (bit-identical to the reference's matmul over a materialised
+        transpose, which lm_direct=False performs per call, as gpt2.rs:395
+        does; the CPU baseline times that form)."""
         self.vocab_size, self.n_positions, self.n_embd = vocab_size, n_positions, n_embd
         self.n_layer, self.n_head = n_layer, n_head
         self._arrays = {k: _f32(v) for k, v in sd.items()}
@@ -217,11 +223,12 @@ class OracleModel:
             raise OracleError(e.value.decode())
         self._h = h
         lib().orc_model_set_threads(h, threads)
+        lib().orc_model_set_lm_direct(h, 1 if lm_direct else 0)
 
     @classmethod
-    def from_shape(cls, sd, shape, threads=1):
+    def from_shape(cls, sd, shape, threads=1, lm_direct=True):
         return cls(sd, shape.vocab_size, shape.n_positions, shape.n_embd, shape.n_layer, shape.n_head,
-                   shape.layer_norm_epsilon, threads)
+                   shape.layer_norm_epsilon, threads, lm_direct)
 
     def set_threads(self, threads: int) -> None:
         lib().orc_model_set_threads(self._h, threads)

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(NT) void bdecode_kernel(BdParams p) {
       for (int b = 0; b < B; ++b) {
         const unsigned long long key =
             __hip_atomic_load(p.keys + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t next = key == 0ull ? 0u : ~(uint32_t)(key & 0xffffffffull);
+        const uint32_t next = argmax_key_index(key);
         p.token[b] = next;
         p.ids[(long)b * p.ld_ids + step] = next;
         __hip_atomic_store(p.keys + b, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

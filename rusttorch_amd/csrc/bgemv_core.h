@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "argmax_key.h"
+
 #include "bgemv.h"
 
 namespace rtg {
@@ -104,15 +106,6 @@ struct Tile<W_BF16> {
     return __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16));
   }
 };
-
-// Packed argmax key (argmax_f32, gpt2.rs:858-868): strict '>' from -inf with
-// the first index winning; -inf and NaN never win (key 0).
-__device__ __forceinline__ u64 pack_key(float v, uint32_t idx) {
-  if (!(v > -INFINITY)) return 0ull;
-  uint32_t b = __float_as_uint(v);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((u64)b << 32) | (u64)(~idx);
-}
 
 // Applies the epilogue to v (row m, output n) and returns the value written.
 template <bool COH>
@@ -393,7 +386,7 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
       if constexpr (LNG) t = inv_std * (t - mean * a.ln_s[n]);
       y[j] = store_out<COH>(a, m, n, t);
       if (a.keys) {
-        const u64 k = pack_key(y[j], (uint32_t)n);
+        const u64 k = argmax_key(y[j], (uint32_t)n);
         best = k > best ? k : best;
       }
     }

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <vector>
 
 #include "../../include/rtgpu.h"
@@ -37,7 +38,12 @@ void persistent_state_destroy(PersistentState* s);
 // and finishes the step itself (the finalize kernel's work): the argmax token
 // goes to *token_dev and ids_dev[*step_dev], *pos_dev and *step_dev advance
 // by one, the packed argmax key is cleared.
+// The caller must hold persistent_launch_lock(device) from the first step it
+// enqueues until its stream has drained.
 hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative);
+// One lock per device: persistent steps of two streams in flight at once could
+// each hold part of the CUs and wait on workgroups that cannot start.
+std::mutex& persistent_launch_lock(int device);
 unsigned* persistent_epoch(PersistentState* s);
 unsigned* persistent_err(PersistentState* s);
 // Writes the latest step's per-workgroup timestamps to $RTG_TRACE_FILE (if set).

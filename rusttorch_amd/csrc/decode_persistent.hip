@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
 #include <vector>
 
 #include "decode_persistent.h"
@@ -243,10 +244,20 @@ hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool c
   void* args[] = {&s->p};
   const void* fn = s->plan->kernel;
   if (cooperative) return hipLaunchCooperativeKernel(fn, dim3(pk::G), dim3(pk::NTHREADS), args, 0, stream);
-  // Inside a captured graph: a plain launch of one workgroup per CU (the
-  // kernel's LDS footprint admits no second one per CU), all co-resident on
-  // an otherwise idle device; every wait is bounded should that not hold.
+  // A plain launch of one workgroup per CU (the kernel's LDS footprint admits
+  // no second one per CU). The workgroups wait on each other, so they must all
+  // become resident: the caller holds persistent_launch_lock for the device
+  // from the first step it enqueues until its stream has drained, so no other
+  // persistent step of this process can take part of the CUs meanwhile.
+  // Ordinary kernels of other streams finish by themselves and only delay the
+  // step; every wait is bounded should residency still fail (another process
+  // on the same GPU), and the host then reports an error.
   return hipLaunchKernel(fn, dim3(pk::G), dim3(pk::NTHREADS), args, 0, stream);
+}
+
+std::mutex& persistent_launch_lock(int device) {
+  static std::mutex locks[64];
+  return locks[(unsigned)device % 64u];
 }
 
 }  // namespace rtg

@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "argmax_key.h"
 #include "kernels.h"
 
 namespace rtg {
@@ -1047,12 +1048,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         const int n = row0 + lr;
         const float v = inv_std * (row_acc<GL>(sm, lr) - mean * sl[k]) + cl[k];
         PK_GW(float, p.logits)[n] = v;
-        u64 key = 0ull;
-        if (v > -INFINITY) {  // -inf and NaN never win (strict '>' from -inf)
-          uint32_t b = __float_as_uint(v);
-          b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-          key = ((u64)b << 32) | (u64)(~(uint32_t)n);
-        }
+        const u64 key = argmax_key(v, (uint32_t)n);  // -inf and NaN give 0: they never win
         best = key > best ? key : best;
       }
     }
@@ -1076,7 +1072,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
                                                       __HIP_MEMORY_SCOPE_AGENT);
       if (arrived == G - 1) {
         const u64 key = __hip_atomic_load(PK_GW(u64, p.keys), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t next = key == 0ull ? 0u : ~(uint32_t)(key & 0xffffffffull);
+        const uint32_t next = argmax_key_index(key);
         const int step = *PK_G(int, p.step);
         PK_GW(uint32_t, p.token)[0] = next;
         PK_GW(uint32_t, p.ids_out)[step] = next;

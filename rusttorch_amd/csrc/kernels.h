@@ -40,7 +40,8 @@ void launch_embed(hipStream_t s, const void* wte, int wtype, const float* wpe, c
 void launch_layernorm(hipStream_t s, const float* x, const float* w, const float* b, float eps, int rows, int d,
                       float* out);
 
-// Decode GEMV: y[b][n] = epi(sum_k x[b][k] * W[n][k]) for b < B (B <= 16).
+// Decode GEMV: y[b][n] = epi(sum_k x[b][k] * W[n][k]) for b < B (any B: more
+// than 16 sequences run as slices of 16).
 void launch_gemv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
                  float* y, int ldy, int N, int K, int epi);
 // Decode QKV GEMV: q part to q[b][d]; k/v parts into the cache at *pos_dev.

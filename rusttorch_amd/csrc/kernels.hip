@@ -10,6 +10,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include "argmax_key.h"
 #include "attn_core.h"
 #include "kernels.h"
 
@@ -316,14 +317,29 @@ static void gemv_dispatch_r(hipStream_t s, const void* W, const float* bias, con
   }
 }
 
+// A launch covers at most 16 sequences (BM); larger batches run as slices of
+// 16 with x, the outputs and the cache rows offset to the slice's first
+// sequence.
 template <int WT>
 static void gemv_dispatch_b(hipStream_t s, int nb, const void* W, const float* bias, const float* x, int ldx, int N,
                             int K, const GemvOut& o) {
-  if (nb <= 1) gemv_dispatch_r<1, WT>(s, W, bias, x, ldx, nb, N, K, o);
-  else if (nb <= 2) gemv_dispatch_r<2, WT>(s, W, bias, x, ldx, nb, N, K, o);
-  else if (nb <= 4) gemv_dispatch_r<4, WT>(s, W, bias, x, ldx, nb, N, K, o);
-  else if (nb <= 8) gemv_dispatch_r<8, WT>(s, W, bias, x, ldx, nb, N, K, o);
-  else gemv_dispatch_r<16, WT>(s, W, bias, x, ldx, nb, N, K, o);
+  for (int b0 = 0; b0 < nb; b0 += 16) {
+    const int n = nb - b0 < 16 ? nb - b0 : 16;
+    GemvOut so = o;
+    if (so.y) so.y += (size_t)b0 * so.ldy;
+    if (so.q) {
+      so.q += (size_t)b0 * so.ldq;
+      const size_t seq = (size_t)so.kv.n_head * so.kv.n_pos * (so.d / so.kv.n_head);
+      so.kv.k += b0 * seq;
+      so.kv.v += b0 * seq;
+    }
+    const float* sx = x + (size_t)b0 * ldx;
+    if (n <= 1) gemv_dispatch_r<1, WT>(s, W, bias, sx, ldx, n, N, K, so);
+    else if (n <= 2) gemv_dispatch_r<2, WT>(s, W, bias, sx, ldx, n, N, K, so);
+    else if (n <= 4) gemv_dispatch_r<4, WT>(s, W, bias, sx, ldx, n, N, K, so);
+    else if (n <= 8) gemv_dispatch_r<8, WT>(s, W, bias, sx, ldx, n, N, K, so);
+    else gemv_dispatch_r<16, WT>(s, W, bias, sx, ldx, n, N, K, so);
+  }
 }
 
 void launch_gemv(hipStream_t s, int B, const void* W, int wtype, const float* bias, const float* x, int ldx,
@@ -427,20 +443,9 @@ void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const flo
 
 // ---------------------------------------------------------------------------
 // Argmax (argmax_f32, gpt2.rs:858-868): strict '>' from -inf, first index wins,
-// NaN never wins. Packed key = (orderable(f) << 32) | ~idx, reduced with a
-// 64-bit atomic max; key 0 (nothing > -inf) decodes to index 0.
+// NaN never wins, -0.0 ties with +0.0. Packed keys (argmax_key.h) reduced with
+// a 64-bit atomic max; key 0 (nothing > -inf) decodes to index 0.
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ unsigned long long pack_key(float v, uint32_t idx) {
-  if (!(v > -INFINITY)) return 0ull;  // -inf and NaN never win
-  uint32_t b = __float_as_uint(v);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((unsigned long long)b << 32) | (unsigned long long)(~idx);
-}
-
-__device__ __forceinline__ uint32_t unpack_idx(unsigned long long key) {
-  return key == 0ull ? 0u : ~(uint32_t)(key & 0xffffffffull);
-}
 
 __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, long ld, int V,
                                                      unsigned long long* keys) {
@@ -449,7 +454,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ l
   const float* p = logits + (size_t)row * ld;
   unsigned long long best = 0ull;
   for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < V; j += gridDim.x * blockDim.x) {
-    unsigned long long k = pack_key(p[j], (uint32_t)j);
+    const unsigned long long k = argmax_key(p[j], (uint32_t)j);
     best = k > best ? k : best;
   }
 #pragma unroll
@@ -471,19 +476,20 @@ void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V,
   argmax_kernel<<<dim3(blocks, rows), 256, 0, s>>>(logits, ld, V, keys);
 }
 
-__global__ void finalize_kernel(int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
-                                int* pos_dev, int* step_dev, unsigned* epoch) {
-  const int b = threadIdx.x;
+// One block of 256 threads, striding over any number of sequences.
+__global__ __launch_bounds__(256) void finalize_kernel(int B, unsigned long long* keys, uint32_t* token,
+                                                       uint32_t* ids_out, int ld_ids, int* pos_dev, int* step_dev,
+                                                       unsigned* epoch) {
   const int step = *step_dev;
   __syncthreads();
-  if (b < B) {
-    const uint32_t t = unpack_idx(keys[b]);
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    const uint32_t t = argmax_key_index(keys[b]);
     token[b] = t;
     if (ids_out) ids_out[(size_t)b * ld_ids + step] = t;
     keys[b] = 0ull;
   }
   __syncthreads();
-  if (b == 0) {
+  if (threadIdx.x == 0) {
     *pos_dev += 1;
     *step_dev = step + 1;
     if (epoch) *epoch += 1u;
@@ -492,26 +498,25 @@ __global__ void finalize_kernel(int B, unsigned long long* keys, uint32_t* token
 
 void launch_finalize(hipStream_t s, int B, unsigned long long* keys, uint32_t* token, uint32_t* ids_out, int ld_ids,
                      int* pos_dev, int* step_dev, unsigned* epoch) {
-  finalize_kernel<<<1, 64, 0, s>>>(B, keys, token, ids_out, ld_ids, pos_dev, step_dev, epoch);
+  finalize_kernel<<<1, 256, 0, s>>>(B, keys, token, ids_out, ld_ids, pos_dev, step_dev, epoch);
 }
 
-__global__ void keys_to_tokens_kernel(int B, unsigned long long* keys, uint32_t* token) {
-  const int b = threadIdx.x;
-  if (b < B) {
-    token[b] = unpack_idx(keys[b]);
+__global__ __launch_bounds__(256) void keys_to_tokens_kernel(int B, unsigned long long* keys, uint32_t* token) {
+  for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < B; b += gridDim.x * blockDim.x) {
+    token[b] = argmax_key_index(keys[b]);
     keys[b] = 0ull;
   }
 }
 
 void launch_keys_to_tokens(hipStream_t s, int B, unsigned long long* keys, uint32_t* token) {
-  keys_to_tokens_kernel<<<1, 64, 0, s>>>(B, keys, token);
+  keys_to_tokens_kernel<<<1, 256, 0, s>>>(B, keys, token);
 }
 
-__global__ void reset_keys_kernel(int B, unsigned long long* keys) {
-  if ((int)threadIdx.x < B) keys[threadIdx.x] = 0ull;
+__global__ __launch_bounds__(256) void reset_keys_kernel(int B, unsigned long long* keys) {
+  for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < B; b += gridDim.x * blockDim.x) keys[b] = 0ull;
 }
 
-void launch_reset_keys(hipStream_t s, int B, unsigned long long* keys) { reset_keys_kernel<<<1, 64, 0, s>>>(B, keys); }
+void launch_reset_keys(hipStream_t s, int B, unsigned long long* keys) { reset_keys_kernel<<<1, 256, 0, s>>>(B, keys); }
 
 // ---------------------------------------------------------------------------
 // Prefill GEMM on fp32 MFMA (v_mfma_f32_32x32x2f32):
@@ -1036,18 +1041,12 @@ static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W,
   return true;
 }
 
-// RTG_GEMM_REG=1 keeps f32 weights on the register-staged gemm_kernel (for A/B timing).
-static bool gemm_reg_forced() {
-  static const bool v = getenv("RTG_GEMM_REG") != nullptr;
-  return v;
-}
-
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
                  long ldc, int M, int N, int K, int epi) {
   if (launch_skinny(s, A, lda, W, wtype, bias, C, ldc, M, N, K, epi, SkinnyQkv{})) return;
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
   if (wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
-      (reinterpret_cast<uintptr_t>(W) & 15) == 0 && !gemm_reg_forced())
+      (reinterpret_cast<uintptr_t>(W) & 15) == 0)
     // (256 x 128 tiles with 3 stages, bounded to two waves per SIMD, were 2-4%
     // faster on the c4 shapes without an epilogue but made the c4 prefill
     // slower, 70.7k against 72.5k tokens/s; 3 stages at three waves per SIMD
@@ -1062,7 +1061,7 @@ void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int 
                      long ldc, int M, int K, int S, int T, int past, KvDst kv) {
   const int N = 3 * kv.d;
   if (M > 64 && wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
-      (reinterpret_cast<uintptr_t>(W) & 15) == 0 && kv.d == 64 * kv.n_head && !gemm_reg_forced()) {
+      (reinterpret_cast<uintptr_t>(W) & 15) == 0 && kv.d == 64 * kv.n_head) {
     const int nb = ((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM);
     gemm_lds_kernel<<<nb, 256, 0, s>>>(A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, EPI_BIAS,
                                        N > M ? 1 : 0, kv, T, past);

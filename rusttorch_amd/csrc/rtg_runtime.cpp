@@ -45,6 +45,10 @@ std::string fmt(const char* f, ...) {
   return buf;
 }
 
+// A C++ exception other than HipError (e.g. std::bad_alloc for a malformed
+// tensor shape) as an error result: no exception crosses the C boundary.
+rtg_result err_internal(const std::exception& ex) { return err(std::string("internal error: ") + ex.what()); }
+
 struct HipError {
   std::string msg;
 };
@@ -229,7 +233,7 @@ static rtg_cache* cache_create(const rtg_model* m, size_t batch) {
     HIPX(hipMemsetAsync(c->step_dev, 0, 256, c->stream));
     launch_reset_keys(c->stream, (int)batch, c->keys);
     HIPX(hipStreamSynchronize(c->stream));
-  } catch (const HipError&) {
+  } catch (...) {
     rtg_cache_destroy(c.release());
     throw;
   }
@@ -743,6 +747,11 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
     destroy_graph(c);  // the step graph changes shape
   }
   prepare_decode(c);
+  // The persistent step's workgroups wait on each other: no second persistent
+  // step of this process may be in flight on the device (another thread's
+  // cache) until this stream has drained.
+  std::unique_lock<std::mutex> plock;
+  if (c->pstate) plock = std::unique_lock<std::mutex>(persistent_launch_lock(m->device));
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
   HIPX(hipEventRecord(c->ev[0], s));
   enqueue_prefill(c, c->ids_in, B, n, 0, 0);
@@ -1003,7 +1012,9 @@ rtg_result build_model(const rtg_config* cfg, Lookup& lk, rtg_storage storage, r
     staging = nullptr;
   } catch (const HipError& he) {
     if (staging) hipFree(staging);
-    return err(he.msg);
+    return err(he.msg);  } catch (const std::exception& ex) {
+    if (staging) hipFree(staging);
+    return err_internal(ex);
   }
   size_t np = V * d + P * d + 2 * d;
   np += L * (2 * d + d * 3 * d + 3 * d + d * d + d + 2 * d + d * 4 * d + 4 * d + 4 * d * d + d);
@@ -1051,52 +1062,60 @@ void rtg_free_error_message(char* msg) { free(msg); }
 
 rtg_result rtg_model_from_host(const rtg_config* cfg, const rtg_named_tensor* tensors, size_t n, rtg_storage storage,
                                rtg_model** out) {
-  if (!cfg || !out) return err("null argument");
-  Lookup lk;
-  for (size_t i = 0; i < n; ++i) {
-    const rtg_named_tensor& t = tensors[i];
-    HostTensor& h = lk[t.name];
-    h.shape.assign(t.shape, t.shape + t.ndim);
-    switch (t.dtype) {
-      case RTG_F32: h.stype = SRC_F32; h.data = t.data; break;
-      case RTG_BF16: h.stype = SRC_BF16; h.data = t.data; break;
-      case RTG_F16: h.stype = SRC_F16; h.data = t.data; break;
-      case RTG_F64:
-        decode_f64(t.data, h.numel(), &h.owned);
-        h.stype = SRC_F32;
-        h.data = h.owned.data();
-        break;
-      default: return err("Unsupported dtype for " + std::string(t.name));
+  try {
+    if (!cfg || !out) return err("null argument");
+    Lookup lk;
+    for (size_t i = 0; i < n; ++i) {
+      const rtg_named_tensor& t = tensors[i];
+      HostTensor& h = lk[t.name];
+      h.shape.assign(t.shape, t.shape + t.ndim);
+      switch (t.dtype) {
+        case RTG_F32: h.stype = SRC_F32; h.data = t.data; break;
+        case RTG_BF16: h.stype = SRC_BF16; h.data = t.data; break;
+        case RTG_F16: h.stype = SRC_F16; h.data = t.data; break;
+        case RTG_F64:
+          decode_f64(t.data, h.numel(), &h.owned);
+          h.stype = SRC_F32;
+          h.data = h.owned.data();
+          break;
+        default: return err("Unsupported dtype for " + std::string(t.name));
+      }
     }
+    return build_model(cfg, lk, storage, out);
+  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
-  return build_model(cfg, lk, storage, out);
 }
 
 rtg_result rtg_model_from_safetensors(const char* path, const rtg_config* cfg, rtg_storage storage,
                                       rtg_model** out) {
-  if (!cfg || !out || !path) return err("null argument");
-  StFile f;
-  std::string e = st_read_file(path, &f);
-  if (!e.empty()) return err("Failed to load safetensors: " + e);
-  // F32, BF16 and F16 tensors are used in place in the mapping (no host copy);
-  // other element types are decoded to f32 (safetensors.rs:232-348).
-  Lookup lk;
-  for (auto& kv : f.entries) {
-    const StEntry& en = kv.second;
-    HostTensor& h = lk[kv.first];
-    h.shape = en.shape;
-    if (en.dtype == "F32" || en.dtype == "BF16" || en.dtype == "F16") {
-      e = st_check_size(en, en.dtype == "F32" ? 4 : 2, en.dtype.c_str());
-      h.stype = en.dtype == "F32" ? SRC_F32 : en.dtype == "BF16" ? SRC_BF16 : SRC_F16;
-      h.data = st_data(f, en);
-    } else {
-      e = st_decode_f32(f, en, &h.owned);
-      h.stype = SRC_F32;
-      h.data = h.owned.data();
-    }
+  try {
+    if (!cfg || !out || !path) return err("null argument");
+    StFile f;
+    std::string e = st_read_file(path, &f);
     if (!e.empty()) return err("Failed to load safetensors: " + e);
+    // F32, BF16 and F16 tensors are used in place in the mapping (no host copy);
+    // other element types are decoded to f32 (safetensors.rs:232-348).
+    Lookup lk;
+    for (auto& kv : f.entries) {
+      const StEntry& en = kv.second;
+      HostTensor& h = lk[kv.first];
+      h.shape = en.shape;
+      if (en.dtype == "F32" || en.dtype == "BF16" || en.dtype == "F16") {
+        e = st_check_size(en, en.dtype == "F32" ? 4 : 2, en.dtype.c_str());
+        h.stype = en.dtype == "F32" ? SRC_F32 : en.dtype == "BF16" ? SRC_BF16 : SRC_F16;
+        h.data = st_data(f, en);
+      } else {
+        e = st_decode_f32(f, en, &h.owned);
+        h.stype = SRC_F32;
+        h.data = h.owned.data();
+      }
+      if (!e.empty()) return err("Failed to load safetensors: " + e);
+    }
+    return build_model(cfg, lk, storage, out);
+  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
-  return build_model(cfg, lk, storage, out);
 }
 
 void rtg_model_destroy(rtg_model* model) { delete model; }
@@ -1109,7 +1128,8 @@ rtg_result rtg_cache_new(const rtg_model* model, size_t batch, rtg_cache** out) 
   try {
     *out = cache_create(model, batch);
   } catch (const HipError& e) {
-    return err(e.msg);
+    return err(e.msg);  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
   return ok();
 }
@@ -1146,7 +1166,8 @@ rtg_result rtg_cache_read(const rtg_cache* c, size_t layer, size_t head, size_t 
   try {
     if (c->len) HIPX(hipMemcpy(out, base, c->len * hd * 4, hipMemcpyDeviceToHost));
   } catch (const HipError& e) {
-    return err(e.msg);
+    return err(e.msg);  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
   return ok();
 }
@@ -1160,7 +1181,8 @@ rtg_result rtg_forward_cached_batched(const rtg_model* model, rtg_cache* cache, 
   try {
     forward_cached_impl(cache, ids, n, logits_out);
   } catch (const HipError& he) {
-    return err(he.msg);
+    return err(he.msg);  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
   return ok();
 }
@@ -1183,7 +1205,8 @@ rtg_result rtg_forward(const rtg_model* model, const uint32_t* ids, size_t n, fl
     PoolLease lease(model, 1);
     forward_cached_impl(lease.c, ids, n, logits_out);
   } catch (const HipError& he) {
-    return err(he.msg);
+    return err(he.msg);  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
   return ok();
 }
@@ -1203,7 +1226,8 @@ rtg_result rtg_generate_cached_batched(const rtg_model* model, const uint32_t* p
   try {
     generate_greedy(model, prompts, batch, n, max_new, out, timing);
   } catch (const HipError& he) {
-    return err(he.msg);
+    return err(he.msg);  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
   return ok();
 }
@@ -1223,7 +1247,8 @@ rtg_result rtg_generate_cached(const rtg_model* model, const uint32_t* prompt, s
   try {
     generate_greedy(model, prompt, 1, n, max_new, out, nullptr, &sp);
   } catch (const HipError& he) {
-    return err(he.msg);
+    return err(he.msg);  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
   return ok();
 }
@@ -1244,7 +1269,8 @@ rtg_result rtg_generate_with_config(const rtg_model* model, const uint32_t* prom
   try {
     generate_greedy(model, prompt, 1, n, cfg->max_new_tokens, out, nullptr, &sp);
   } catch (const HipError& he) {
-    return err(he.msg);
+    return err(he.msg);  } catch (const std::exception& ex) {
+    return err_internal(ex);
   }
   return ok();
 }
@@ -1298,7 +1324,10 @@ rtg_result rtg_generate(const rtg_model* model, const uint32_t* prompt, size_t n
   } catch (const HipError& he) {
     if (toks) hipFree(toks);
     if (steps) hipFree(steps);
-    return err(he.msg);
+    return err(he.msg);  } catch (const std::exception& ex) {
+    if (toks) hipFree(toks);
+    if (steps) hipFree(steps);
+    return err_internal(ex);
   }
   hipFree(toks);
   hipFree(steps);

@@ -240,61 +240,70 @@ std::string st_read_file(const std::string& path, StFile* out) {
   return "";
 }
 
+// Element count of e's shape; false when the product overflows.
+static bool st_numel(const StEntry& e, size_t* n) {
+  size_t c = 1;
+  for (size_t s : e.shape)
+    if (__builtin_mul_overflow(c, s, &c)) return false;
+  *n = c;
+  return true;
+}
+
 std::string st_check_size(const StEntry& e, size_t elem_bytes, const char* name) {
-  size_t n = 1;
-  for (size_t s : e.shape) n *= s;
   const size_t len = e.end - e.begin;
-  if (len != n * elem_bytes)
-    return std::string("Invalid safetensors format: ") + name + " tensor: expected " + std::to_string(n * elem_bytes) +
+  size_t n = 0, bytes = 0;
+  if (!st_numel(e, &n) || __builtin_mul_overflow(n, elem_bytes, &bytes))
+    return std::string("Invalid safetensors format: ") + name + " tensor: shape overflows, got " +
+           std::to_string(len) + " bytes";
+  if (len != bytes)
+    return std::string("Invalid safetensors format: ") + name + " tensor: expected " + std::to_string(bytes) +
            " bytes, got " + std::to_string(len);
   return "";
 }
 
 std::string st_decode_f32(const StFile& f, const StEntry& e, std::vector<float>* out) {
-  size_t n = 1;
-  for (size_t s : e.shape) n *= s;
+  // the byte count is checked against the shape before anything is allocated
+  size_t w = 0;
+  const char* name = nullptr;
+  if (e.dtype == "F32" || e.dtype == "I32") w = 4, name = e.dtype == "F32" ? "F32" : "I32";
+  else if (e.dtype == "F64" || e.dtype == "I64") w = 8, name = e.dtype == "F64" ? "F64" : "I64";
+  else if (e.dtype == "F16" || e.dtype == "BF16") w = 2, name = e.dtype == "F16" ? "F16" : "BF16";
+  else if (e.dtype == "U8" || e.dtype == "BOOL") w = 1, name = "U8";
+  else return "Unsupported dtype: " + e.dtype;
+  const std::string err = st_check_size(e, w, name);
+  if (!err.empty()) return err;
+  const size_t n = (e.end - e.begin) / w;
   const uint8_t* raw = st_data(f, e);
   out->resize(n);
-  auto need = [&](size_t w, const char* name) { return st_check_size(e, w, name); };
-  std::string err;
   if (e.dtype == "F32") {
-    if (!(err = need(4, "F32")).empty()) return err;
     memcpy(out->data(), raw, n * 4);
   } else if (e.dtype == "F64") {
-    if (!(err = need(8, "F64")).empty()) return err;
     for (size_t i = 0; i < n; ++i) {
       double v;
       memcpy(&v, raw + 8 * i, 8);
       (*out)[i] = (float)v;
     }
   } else if (e.dtype == "F16") {
-    if (!(err = need(2, "F16")).empty()) return err;
     for (size_t i = 0; i < n; ++i) (*out)[i] = f16_to_f32((uint16_t)(raw[2 * i] | (raw[2 * i + 1] << 8)));
   } else if (e.dtype == "BF16") {
-    if (!(err = need(2, "BF16")).empty()) return err;
     for (size_t i = 0; i < n; ++i) {
       uint32_t b = (uint32_t)(raw[2 * i] | (raw[2 * i + 1] << 8)) << 16;
       memcpy(&(*out)[i], &b, 4);
     }
   } else if (e.dtype == "I32") {
-    if (!(err = need(4, "I32")).empty()) return err;
     for (size_t i = 0; i < n; ++i) {
       int32_t v;
       memcpy(&v, raw + 4 * i, 4);
       (*out)[i] = (float)v;
     }
   } else if (e.dtype == "I64") {
-    if (!(err = need(8, "I64")).empty()) return err;
     for (size_t i = 0; i < n; ++i) {
       int64_t v;
       memcpy(&v, raw + 8 * i, 8);
       (*out)[i] = (float)v;
     }
-  } else if (e.dtype == "U8" || e.dtype == "BOOL") {
-    if (!(err = need(1, "U8")).empty()) return err;
+  } else {  // U8, BOOL
     for (size_t i = 0; i < n; ++i) (*out)[i] = (float)raw[i];
-  } else {
-    return "Unsupported dtype: " + e.dtype;
   }
   return "";
 }

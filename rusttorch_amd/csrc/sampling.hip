@@ -37,6 +37,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "argmax_key.h"
 #include "kernels.h"
 
 namespace rtg {
@@ -386,13 +387,13 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
   uint32_t pick = 0;
   if (sp.temperature <= 0.0f) {
     // ---- greedy: argmax_f32 (gpt2.rs:858-868), strict '>' from -inf, the
-    // first index wins, NaN never wins ----
+    // first index wins, NaN never wins, -0.0 ties with +0.0 (argmax_key.h) ----
     unsigned long long best = 0ull;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int i = j * ST + t;
-      if (i < V && v[j] > -INFINITY) {
-        const unsigned long long k = ((unsigned long long)order_key(v[j]) << 32) | (uint32_t)~(uint32_t)i;
+      if (i < V) {
+        const unsigned long long k = argmax_key(v[j], (uint32_t)i);
         best = k > best ? k : best;
       }
     }
@@ -400,7 +401,7 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float* __restrict__ lo
     __syncthreads();
     if (best) atomicMax(&sm.key, best);
     __syncthreads();
-    pick = sm.key ? ~(uint32_t)(sm.key & 0xffffffffull) : 0u;
+    pick = argmax_key_index(sm.key);
   } else {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) v[j] = v[j] / sp.temperature;

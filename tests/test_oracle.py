@@ -301,6 +301,40 @@ def test_gelu_closed_form(O):
     np.testing.assert_allclose(O.gelu_new(x), ref64.gelu_new(x.astype(np.float64)), atol=1e-6)
 
 
+def test_matmul_sums_each_element_in_k_order(O):
+    """orc_matmul's register tiles (4 rows x 32 columns, row groups across
+    threads) leave each element's arithmetic as the plain loop's: start from
+    0.0f, then one rounded f32 product and one rounded f32 add per k in
+    ascending order. numpy's f32 elementwise ops round each op the same way,
+    so the results are bit-identical, for every tile remainder and thread
+    count."""
+    rng = np.random.default_rng(11)
+    for m, k, n in [(1, 64, 40), (5, 33, 70), (9, 128, 96), (67, 20, 33)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        ref = np.zeros((m, n), np.float32)
+        for kk in range(k):
+            ref = ref + a[:, kk:kk + 1] * b[kk:kk + 1, :]
+        for th in (1, 3):
+            assert np.array_equal(O.matmul(a, b, threads=th), ref), (m, k, n, th)
+
+
+def test_lm_head_direct_equals_transposed(O):
+    """The oracle's direct LM head (each logit summed from its wte row) gives
+    bit for bit the logits of the reference's form, a matmul over the
+    materialised transpose wte.t().to_owned() (gpt2.rs:395), threaded or not."""
+    from rusttorch_amd import synth
+    sh = synth.SHAPES["mini"]
+    sd = synth.make_weights(sh)
+    ids = synth.make_tokens(9, sh.vocab_size, stream=21)
+    outs = []
+    for direct, th in ((False, 1), (True, 1), (True, 4)):
+        om = O.OracleModel.from_shape(sd, sh, threads=th, lm_direct=direct)
+        c = om.new_cache()
+        outs.append(np.concatenate([om.forward_cached(ids, c), om.forward_cached([3], c)]))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
 def test_matmul_exact_integers(O):  # integer-exact case as in autograd/tests.rs:126-153
     a = np.array([[1, 2], [3, 4]], np.float32)
     b = np.array([[5, 6], [7, 8]], np.float32)
