@@ -261,32 +261,42 @@ static KvDst kv_layer(const rtg_cache* c, size_t l) {
   return kv;
 }
 
+// Activation buffers of one forward pass: x, ln [M][d], qkv [M][3d],
+// att [M][d], h [M][4d] and the logits rows.
+struct Work {
+  float *x, *ln, *qkv, *att, *h, *logits;
+};
+
+static Work cache_work(const rtg_cache* c) { return Work{c->x, c->ln, c->qkv, c->att, c->h, c->logits}; }
+
 // forward_cached body for S sequences x T new tokens (gpt2.rs:376-396) on the
-// MFMA prefill path. ids_dev holds S*T ids; logits rows: all S*T (mode 0) or
-// the last row of each sequence (mode 1, written as S rows).
-static void enqueue_prefill(rtg_cache* c, const uint32_t* ids_dev, size_t S, size_t T, size_t past, int logit_mode) {
+// MFMA prefill path, on the activation buffers w. ids_dev holds S*T ids;
+// logits rows: all S*T (mode 0) or the last row of each sequence (mode 1,
+// written as S rows).
+static void enqueue_prefill(rtg_cache* c, const Work& w, const uint32_t* ids_dev, size_t S, size_t T, size_t past,
+                            int logit_mode) {
   const rtg_model* m = c->m;
   const int d = (int)m->cfg.n_embd, V = (int)m->cfg.vocab_size, M = (int)(S * T);
   const float eps = m->cfg.layer_norm_epsilon;
   hipStream_t s = c->stream;
-  launch_embed(s, m->wte, m->wtype, m->wpe, ids_dev, M, (int)T, (int)past, nullptr, d, c->x);
+  launch_embed(s, m->wte, m->wtype, m->wpe, ids_dev, M, (int)T, (int)past, nullptr, d, w.x);
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const LayerW& L = m->layers[l];
     KvDst kv = kv_layer(c, l);
-    launch_layernorm(s, c->x, L.ln1w, L.ln1b, eps, M, d, c->ln);
-    launch_gemm_qkv(s, c->ln, d, L.wqkv, m->wtype, L.bqkv, c->qkv, 3 * d, M, d, (int)S, (int)T, (int)past, kv);
-    launch_attn_prefill(s, c->qkv, (int)S, (int)T, (int)past, kv.k, kv.v, kv.n_head, kv.n_pos, d, c->att);
-    launch_gemm(s, c->att, d, L.waproj, m->wtype, L.baproj, c->x, d, M, d, d, EPI_BIAS_RESID);
-    launch_layernorm(s, c->x, L.ln2w, L.ln2b, eps, M, d, c->ln);
-    launch_gemm(s, c->ln, d, L.wfc, m->wtype, L.bfc, c->h, 4 * d, M, 4 * d, d, EPI_BIAS_GELU);
-    launch_gemm(s, c->h, 4 * d, L.wmproj, m->wtype, L.bmproj, c->x, d, M, d, 4 * d, EPI_BIAS_RESID);
+    launch_layernorm(s, w.x, L.ln1w, L.ln1b, eps, M, d, w.ln);
+    launch_gemm_qkv(s, w.ln, d, L.wqkv, m->wtype, L.bqkv, w.qkv, 3 * d, M, d, (int)S, (int)T, (int)past, kv);
+    launch_attn_prefill(s, w.qkv, (int)S, (int)T, (int)past, kv.k, kv.v, kv.n_head, kv.n_pos, d, w.att);
+    launch_gemm(s, w.att, d, L.waproj, m->wtype, L.baproj, w.x, d, M, d, d, EPI_BIAS_RESID);
+    launch_layernorm(s, w.x, L.ln2w, L.ln2b, eps, M, d, w.ln);
+    launch_gemm(s, w.ln, d, L.wfc, m->wtype, L.bfc, w.h, 4 * d, M, 4 * d, d, EPI_BIAS_GELU);
+    launch_gemm(s, w.h, 4 * d, L.wmproj, m->wtype, L.bmproj, w.x, d, M, d, 4 * d, EPI_BIAS_RESID);
   }
-  launch_layernorm(s, c->x, m->lnfw, m->lnfb, eps, M, d, c->ln);
+  launch_layernorm(s, w.x, m->lnfw, m->lnfb, eps, M, d, w.ln);
   if (logit_mode == 0) {
-    launch_gemm(s, c->ln, d, m->wte, m->wtype, nullptr, c->logits, V, M, V, d, EPI_NONE);
+    launch_gemm(s, w.ln, d, m->wte, m->wtype, nullptr, w.logits, V, M, V, d, EPI_NONE);
   } else {
     // Last row of each sequence: rows (s*T + T-1), stride T*d.
-    launch_gemm(s, c->ln + (T - 1) * d, (int)(T * d), m->wte, m->wtype, nullptr, c->logits, V, (int)S, V, d,
+    launch_gemm(s, w.ln + (T - 1) * d, (int)(T * d), m->wte, m->wtype, nullptr, w.logits, V, (int)S, V, d,
                 EPI_NONE);
   }
 }
@@ -686,7 +696,7 @@ static void forward_cached_impl(rtg_cache* c, const uint32_t* ids, size_t n, flo
     enqueue_decode_step(c);
   } else {
     HIPX(hipMemcpyAsync(c->ids_in, ids, B * n * 4, hipMemcpyHostToDevice, c->stream));
-    enqueue_prefill(c, c->ids_in, B, n, c->len, 0);
+    enqueue_prefill(c, cache_work(c), c->ids_in, B, n, c->len, 0);
   }
   if (logits_out) HIPX(hipMemcpyAsync(logits_out, c->logits, B * n * V * 4, hipMemcpyDeviceToHost, c->stream));
   HIPX(hipStreamSynchronize(c->stream));
@@ -754,7 +764,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   if (c->pstate) plock = std::unique_lock<std::mutex>(persistent_launch_lock(m->device));
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
   HIPX(hipEventRecord(c->ev[0], s));
-  enqueue_prefill(c, c->ids_in, B, n, 0, 0);
+  enqueue_prefill(c, cache_work(c), c->ids_in, B, n, 0, 0);
   // argmax of the last row of each sequence (extract_row(logits, n-1))
   launch_argmax(s, c->logits + (n - 1) * V, (long)(n * V), (int)B, (int)V, c->keys);
   // finalize advances pos by one: after it, pos = n, the position of the
@@ -1314,7 +1324,7 @@ rtg_result rtg_generate(const rtg_model* model, const uint32_t* prompt, size_t n
     for (size_t i = 0; i < max_new; ++i) {
       const size_t len = n + i;
       const size_t start = len > P ? len - P : 0;
-      enqueue_prefill(c, toks + start, 1, len - start, 0, 1);  // logits of the last row only
+      enqueue_prefill(c, cache_work(c), toks + start, 1, len - start, 0, 1);  // logits of the last row only
       if (!launch_sample(s, c->logits, (int)V, toks, (int)n, toks + n, steps + i, sp, c->token_dev))
         throw HipError{"vocabulary too large for the device sampler"};
     }
