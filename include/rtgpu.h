@@ -130,6 +130,18 @@ rtg_result rtg_forward(const rtg_model* model, const uint32_t* ids, size_t n, fl
  * (may be NULL to skip the device-to-host copy). The cache must have batch 1. */
 rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
                               float* logits_out);
+/* forward_cached without device allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results as rtg_forward_cached, but the activations
+ * and logits of the pass live in a fixed 16 MiB scratch array per device
+ * inside the library instead of the cache's work buffers, and nothing is
+ * allocated. Limit: n * (10 * n_embd + vocab_size) floats (each of the six
+ * parts rounded up to 64) must fit in 16 MiB, e.g. n <= 72 for GPT-2 small;
+ * a larger n returns an error. All calls on one device share the array:
+ * calls that overlap on one device race. */
+rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
+                                      float* logits_out);
 /* Gpt2Model::generate (uncached, sliding window), gpt2.rs:311-346.
  * out receives n + max_new ids. */
 rtg_result rtg_generate(const rtg_model* model, const uint32_t* prompt, size_t n, size_t max_new,

@@ -81,6 +81,7 @@ SIGNATURES = {
     "rtg_cache_read": (Result, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_int, C.c_void_p]),
     "rtg_forward": (Result, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "rtg_forward_cached": (Result, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "rtg_forward_cached_noalloc": (Result, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "rtg_generate": (Result, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_float, C.c_uint64,
                               C.c_void_p]),
     "rtg_generate_cached": (Result, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_float, C.c_uint64,

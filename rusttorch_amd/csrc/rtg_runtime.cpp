@@ -23,6 +23,7 @@
 #include "bgemv.h"
 #include "kernels.h"
 #include "safetensors_reader.h"
+#include "scratch.h"
 
 using namespace rtg;
 
@@ -1201,6 +1202,50 @@ rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const ui
                               float* logits_out) {
   if (cache && cache->batch != 1) return err("rtg_forward_cached needs a batch-1 cache");
   return rtg_forward_cached_batched(model, cache, ids, n, logits_out);
+}
+
+rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
+                                      float* logits_out) {
+  if (!model || !cache || (n && !ids)) return err("null argument");
+  if (cache->batch != 1) return err("rtg_forward_cached_noalloc needs a batch-1 cache");
+  std::string e = check_cached(model, cache->len, ids, n);
+  if (!e.empty()) return err(e);
+  // x, ln, att [n][d], qkv [n][3d], h [n][4d], logits [n][V] in the device's
+  // scratch array, each part on a 256-byte boundary like a hipMalloc'd buffer
+  // (the same alignment, so the same kernels as rtg_forward_cached run)
+  const size_t d = model->cfg.n_embd, V = model->cfg.vocab_size;
+  const size_t pd = align_up(n * d, 64), p3 = align_up(3 * n * d, 64), p4 = align_up(4 * n * d, 64);
+  const size_t need = 3 * pd + p3 + p4 + align_up(n * V, 64);
+  if (need > kScratchFloats)
+    return err(fmt("rtg_forward_cached_noalloc: %zu new tokens need %zu bytes of scratch; it holds %zu", n,
+                   need * 4, kScratchFloats * 4));
+  try {
+    hipError_t he = hipSuccess;
+    float* sp = scratch_device_ptr(model->device, &he);
+    HIPX(he);
+    // Nothing here has to start at zero: every kernel of the pass writes its
+    // output rows in full before they are read (the residual epilogues add
+    // into x after the embedding has written it).
+    Work w;
+    w.x = sp;
+    w.ln = w.x + pd;
+    w.att = w.ln + pd;
+    w.qkv = w.att + pd;
+    w.h = w.qkv + p3;
+    w.logits = w.h + p4;
+    HIPX(hipMemcpyAsync(cache->ids_in, ids, n * 4, hipMemcpyHostToDevice, cache->stream));
+    enqueue_prefill(cache, w, cache->ids_in, 1, n, cache->len, 0);
+    HIPX(hipGetLastError());
+    if (logits_out)
+      HIPX(hipMemcpyAsync(logits_out, w.logits, n * V * 4, hipMemcpyDeviceToHost, cache->stream));
+    HIPX(hipStreamSynchronize(cache->stream));
+    cache->len += n;
+  } catch (const HipError& he) {
+    return err(he.msg);
+  } catch (const std::exception& ex) {
+    return err_internal(ex);
+  }
+  return ok();
 }
 
 rtg_result rtg_forward(const rtg_model* model, const uint32_t* ids, size_t n, float* logits_out) {

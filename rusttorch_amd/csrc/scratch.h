@@ -1,0 +1,19 @@
+// Device scratch for the entry point that allocates nothing
+// (rtg_forward_cached_noalloc): one fixed array per device, in the library's
+// code object, holding the activations and logits of one forward pass.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace rtg {
+
+// 16 MiB: GPT-2 small takes (10 d + V) floats per new token (x, ln, att:
+// d each; qkv 3d; h 4d; one logits row), so 72 tokens fit; XL 63.
+constexpr size_t kScratchFloats = (size_t)4 << 20;
+
+// Device address of `device`'s copy of the array (looked up once per device
+// with hipGetSymbolAddress, with that device current; the current device is
+// restored afterwards). Null with *err set on failure.
+float* scratch_device_ptr(int device, hipError_t* err);
+
+}  // namespace rtg
