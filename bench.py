@@ -71,22 +71,41 @@ def _time_oracle(m, O, prompt, n_decode):
     return t1 - t0, time.perf_counter() - t1
 
 
-def cpu_baseline(sd, sh, prompt, n_decode, all_threads):
-    """Time the CPU oracle (a C restatement of gpt2.rs) on a bounded c1
-    sample: with 1 thread, as the reference's single-threaded ndarray GEMM
-    (the reported value), and with all_threads GEMM threads beside it."""
+# The CPU baseline's bounded sample per workload (BASELINE.md plans subsets
+# for the slow configurations): (prompt tokens timed, decode steps timed,
+# what the sample stands for). The reference runs one sequence at a time, so
+# a batch of B runs B such samples one after another: its tokens/s is the
+# single-sequence rate.
+CPU_SAMPLES = {
+    "c1": (32, 24, "c1's prompt of 32 then 24 of its 63 decode steps"),
+    "c2": (128, 16, "one of c2's 8 sequences: its prompt of 128 then 16 of its 255 decode steps"),
+    "c3": (128, 16, "c3's model: a prompt of 128 (of 512) then 16 decode steps"),
+    "c5": (64, 8, "one of c5's 16 sequences: its prompt of 64 then 8 of its 255 decode steps"),
+    "c4": (128, 0, "one of c4's 32 sequences, its first 128 of 1024 tokens (prefill only)"),
+}
+
+
+def cpu_baseline(sd, sh, prompt, n_decode, all_threads, what):
+    """Time the CPU oracle (a C restatement of gpt2.rs, built -O3 for
+    x86-64-v3, the tied LM head multiplying a transpose materialised per call
+    as gpt2.rs:395 does) on a bounded sample: with 1 thread, as the
+    reference's single-threaded ndarray GEMM (the reported value), and with
+    all_threads GEMM threads beside it."""
     from oracle import oracle as O
     O.build()
-    m = O.OracleModel.from_shape(sd, sh, threads=1)
+    m = O.OracleModel.from_shape(sd, sh, threads=1, lm_direct=False)
     pre, dec = _time_oracle(m, O, prompt, n_decode)
-    out = {"value": n_decode / dec, "unit": "tokens/s", "cores": 1, "kind": "port",
-           "sample": f"c1 prompt {len(prompt)} prefill ({pre * 1e3:.0f} ms) then {n_decode} greedy decode "
-                     f"steps; oracle/gpt2_oracle.c (C restatement of gpt2.rs), 1 thread",
+    rate = (n_decode / dec) if n_decode else len(prompt) / pre
+    out = {"value": rate, "unit": "tokens/s", "cores": 1, "kind": "port",
+           "sample": f"{what}: prefill {pre * 1e3:.0f} ms" + (f", {n_decode} greedy decode steps {dec * 1e3:.0f} ms"
+                                                              if n_decode else "")
+                     + "; oracle/gpt2_oracle.c (C restatement of gpt2.rs), 1 thread",
            "prefill_tok_s": len(prompt) / pre, "cpu": _cpu_model(), "nproc": os.cpu_count()}
     if all_threads > 1:
         m.set_threads(all_threads)
         pre, dec = _time_oracle(m, O, prompt, n_decode)
-        out["all_cores"] = {"threads": all_threads, "value": n_decode / dec, "prefill_tok_s": len(prompt) / pre}
+        out["all_cores"] = {"threads": all_threads, "value": (n_decode / dec) if n_decode else len(prompt) / pre,
+                            "prefill_tok_s": len(prompt) / pre}
     return out
 
 
@@ -114,7 +133,6 @@ def run_prefill(a):
     sd = synth.make_weights(sh)
     cfg = Gpt2Config(sh.vocab_size, sh.n_positions, sh.n_embd, sh.n_layer, sh.n_head, sh.layer_norm_epsilon)
     m = Gpt2Model.from_state_dict(sd, cfg)
-    del sd
     ids = np.stack([synth.make_tokens(T, sh.vocab_size, stream=b) for b in range(B)])
     cache = m.new_cache(B)
     print("[bench] model resident; warming up", file=sys.stderr, flush=True)
@@ -128,6 +146,7 @@ def run_prefill(a):
         m.forward_cached_batched(ids, cache, want_logits=False)  # logits stay in HBM
         times.append(time.perf_counter() - t0)
     print("[bench] timed steps done", file=sys.stderr, flush=True)
+    del m
     step_s = float(np.mean(times))
     flops = prefill_flops(sh, B, T)
     achieved = flops / step_s / 1e12
@@ -147,21 +166,54 @@ def run_prefill(a):
                      "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), "flops_per_step": flops,
                      "traffic": None},
     }
+    if not a.no_cpu:
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        n_cpu, _, what = CPU_SAMPLES[a.workload]
+        out["cpu_baseline"] = cpu_baseline(sd, sh, ids[0, :n_cpu], 0, a.cpu_threads, what)
     print(json.dumps(out))
 
 
-def measured_traffic(workload):
-    """HBM bytes per decode_step_kernel launch measured by the rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (scaled by the
-    copy-kernel calibration recorded there); None when no summary exists."""
-    path = os.path.join(ROOT, "profiles", f"decode_step_kernel_{workload}_hbm_traffic.md")
+def measured_traffic(workload, persistent):
+    """HBM bytes per decode step measured by the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes summarised in profiles/ (scaled by the copy-kernel
+    calibration recorded there): per decode_step_kernel launch at batch 1,
+    summed over the kernels of one step of the batched graph otherwise; None
+    when no summary exists."""
+    name = f"decode_step_kernel_{workload}" if persistent else f"decode_step_graph_{workload}"
+    path = os.path.join(ROOT, "profiles", f"{name}_hbm_traffic.md")
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith("traffic_bytes_per_launch:") or line.startswith("traffic_bytes_per_step:"):
                 return int(line.split(":")[1])
     except OSError:
         pass
     return None
+
+
+def prefill_bytes(sh, B, T, wbytes):
+    """Algorithmic HBM bytes of forward_cached over T tokens on an empty
+    cache: weights once, the T embedding rows, the K/V rows written and every
+    row's logits written (the reference computes [T, V])."""
+    L, d, V = sh.n_layer, sh.n_embd, sh.vocab_size
+    weights = (L * (12 * d * d + 13 * d) + V * d + 2 * d)
+    mats = L * 12 * d * d + V * d
+    wb = mats * wbytes + (weights - mats) * 4
+    return wb + B * T * (2 * d * wbytes + L * 2 * d * 4 + V * 4)
+
+
+def prefill_roofline(sh, B, T, wbytes, ms):
+    """Roofline of the prefill leg: HBM when its arithmetic intensity is
+    below the fp32 ridge (157.3 TFLOP/s / 8 TB/s), MFMA fp32 otherwise."""
+    flops = prefill_flops(sh, B, T)
+    nbytes = prefill_bytes(sh, B, T, wbytes)
+    s = ms / 1e3
+    if flops / nbytes < MFMA_FP32_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+        ach = nbytes / s / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "bytes": int(nbytes), "ms": round(ms, 4)}
+    ach = flops / s / 1e12
+    return {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / MFMA_FP32_PEAK_TFLOPS, 4), "flops": int(flops), "ms": round(ms, 4)}
 
 
 def calib_copy(nbytes):
@@ -254,7 +306,7 @@ def main():
         kernel = "decode step (graph of per-op kernels: tile-ordered GEMVs, fused attention)"
     dur_ms = step_ms
     achieved = avg_bytes / (dur_ms / 1e3) / 1e9
-    traffic = measured_traffic(a.workload) if persistent else None
+    traffic = measured_traffic(a.workload, persistent)
     out = {
         "metric": METRIC,
         "value": round(dec_tok_s, 2),
@@ -271,15 +323,20 @@ def main():
         "config": {"workload": f"{a.workload}: GPT-2 {shape_name}, batch {B}, prompt {n_prompt}, greedy {n_new}",
                    "batch": B, "prompt": n_prompt, "new_tokens": n_new, "weights": storage},
         "prefill_tok_s": round(B * n_prompt * a.steps / (pre_ms / 1e3), 1),
+        "prefill_roofline": prefill_roofline(sh, B, n_prompt, wbytes, pre_ms / a.steps),
         "decode_ms_per_token_step": round(step_ms, 4),
         "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "bytes_per_launch": int(avg_bytes), "avg_launch_ms": round(dur_ms, 5), "traffic": traffic},
         "first_ids": ids[0, n_prompt:n_prompt + 8].tolist(),
     }
-    if not a.no_cpu and a.workload == "c1":
+    if not a.no_cpu:
         print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(sd, sh, prompts[0], a.cpu_decode_steps, a.cpu_threads)
+        del m
+        n_cpu, n_dec, what = CPU_SAMPLES[a.workload]
+        if a.workload == "c1":
+            n_dec = a.cpu_decode_steps
+        out["cpu_baseline"] = cpu_baseline(sd, sh, prompts[0, :n_cpu], n_dec, a.cpu_threads, what)
     print(json.dumps(out))
 
 

@@ -55,11 +55,20 @@ __global__ void tile_weights_kernel(const void* __restrict__ src, int wtype, int
   reinterpret_cast<u4v*>(dst)[i] = v;
 }
 
-template <int WT, int NPW, bool LNG>
+template <int WT, int NPW, bool LNG, int DEPTH, bool ONESHOT>
 __global__ __launch_bounds__(64 * BG_NW) void bgemv_kernel(BgemvArgs a) {
   __shared__ float red[BG_NW][NPW][256];
   __shared__ unsigned last;
-  bgc::bgemv_unit<WT, NPW, LNG, BG_NW, false>(a, blockIdx.x, blockIdx.y, red, &last);
+  bgc::bgemv_unit<WT, NPW, LNG, BG_NW, false, DEPTH, ONESHOT>(a, blockIdx.x, blockIdx.y, red, &last);
+}
+
+// k-tiles a wave keeps in flight: its whole chunk at once when that fits
+// the register budget (about 160 registers of tiles), else a ring of 4.
+int bgemv_depth(const BgemvPlan& pl, int wtype, bool lng) {
+  const int per_tile = 4 * pl.npw + (wtype == W_F32 ? 4 : 8) * (lng ? 2 : 1);
+  for (int d : {8, 12})
+    if (pl.ktc <= d && per_tile * d <= 160) return d;
+  return 4;
 }
 
 // Decode embedding of B rows (gpt2.rs:377-384: wte[token] + wpe[position])
@@ -168,10 +177,17 @@ bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
   a.ktc = pl.ktc;
   const dim3 grid(pl.groups, pl.S);
   const dim3 block(64 * BG_NW);
-#define BG_LAUNCH(WT, NPW)                                   \
-  do {                                                       \
-    if (a.ln_g) bgemv_kernel<WT, NPW, true><<<grid, block, 0, s>>>(a); \
-    else bgemv_kernel<WT, NPW, false><<<grid, block, 0, s>>>(a);       \
+  const int depth = bgemv_depth(pl, a.wtype, a.ln_g != nullptr);
+#define BG_LAUNCH_D(WT, NPW, LNG)                                                         \
+  do {                                                                                    \
+    if (depth == 12) bgemv_kernel<WT, NPW, LNG, 12, true><<<grid, block, 0, s>>>(a);      \
+    else if (depth == 8) bgemv_kernel<WT, NPW, LNG, 8, true><<<grid, block, 0, s>>>(a);   \
+    else bgemv_kernel<WT, NPW, LNG, 4, false><<<grid, block, 0, s>>>(a);                  \
+  } while (0)
+#define BG_LAUNCH(WT, NPW)                 \
+  do {                                     \
+    if (a.ln_g) BG_LAUNCH_D(WT, NPW, true); \
+    else BG_LAUNCH_D(WT, NPW, false);       \
   } while (0)
   if (a.wtype == W_F32) {
     if (pl.npw == 1) BG_LAUNCH(W_F32, 1);
@@ -183,6 +199,7 @@ bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
     else BG_LAUNCH(W_BF16, 4);
   }
 #undef BG_LAUNCH
+#undef BG_LAUNCH_D
   return hipGetLastError() == hipSuccess;
 }
 

@@ -24,7 +24,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 typedef unsigned u4v __attribute__((ext_vector_type(4)));
 typedef unsigned long long u64;
 
-constexpr int DEPTH = 4;    // k-tiles in flight per wave
+constexpr int DEPTH = 4;    // k-tiles in flight per wave of the streaming (ring) form
 constexpr int SMAX = 8;     // most workgroups per panel group
 constexpr int LNG_PER = 8;  // statistics groups per lane (ln_groups <= 128)
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -205,7 +205,10 @@ __device__ __forceinline__ void row_stats_merge(const BgemvArgs& a, const float2
 // One work unit = panel group g, k split s, on the NW waves of this
 // workgroup (wave w takes k-chunk s * NW + w). red: LDS [NW][NPW][256];
 // last: one LDS word. Every thread of the workgroup calls it.
-template <int WT, int NPW, bool LNG, int NW, bool COH>
+// DEPTH_ k-tiles of a wave are in flight at once: a ring refilled as tiles
+// are consumed, or, with ONESHOT (the caller guarantees ktc <= DEPTH_), the
+// whole chunk loaded at once and consumed without refills.
+template <int WT, int NPW, bool LNG, int NW, bool COH, int DEPTH_ = DEPTH, bool ONESHOT = false>
 __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, float (*red)[NPW][256],
                                            unsigned* last) {
   typedef Tile<WT> TL;
@@ -234,11 +237,11 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
 #pragma unroll
   for (int j = 0; j < NPW; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // ring of DEPTH tiles in flight; past the end the last tile is re-read
-  // (never consumed) so that the load sequence stays branch-free
-  Raw w[DEPTH][NPW];
-  f4v x[DEPTH][E / 4];
-  f4v gv[LNG ? DEPTH : 1][E / 4];
+  // DEPTH_ tiles in flight; past the end the last tile is re-read (never
+  // consumed) so that the load sequence stays branch-free
+  Raw w[DEPTH_][NPW];
+  f4v x[DEPTH_][E / 4];
+  f4v gv[LNG ? DEPTH_ : 1][E / 4];
   auto issue = [&](int slot, int i) {
     const int ti = min(i, max(nt - 1, 0));
 #pragma unroll
@@ -250,12 +253,46 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
       if constexpr (LNG) gv[slot][h] = *reinterpret_cast<const f4v*>(grow + ti * TK + 4 * h);
     }
   };
+  // one tile: acc += x . w over its TK inputs
+  auto consume = [&](int d) {
+    if constexpr (WT == W_BF16) {
+      // bf16 weights: the tile is one v_mfma_f32_16x16x32_bf16 B operand;
+      // x enters as three exact bf16 parts, so every product w * part is
+      // exact in f32 and the MFMA accumulates in f32: the f32 GEMV up to
+      // summation order (3 MFMAs per tile instead of 8 of 16x16x4 f32;
+      // measured ~10% faster, with half the error against a float64 sum)
+      float xs[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xs[e] = x[d][e >> 2][e & 3];
+        if constexpr (LNG) xs[e] *= gv[d][e >> 2][e & 3];
+      }
+      u4v xh, xm, xl;
+      split3(xs, xh, xm, xl);
+#pragma unroll
+      for (int j = 0; j < NPW; ++j) {
+        const bf16x8 wb = as_bf16x8(w[d][j]);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xh), wb, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xm), wb, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xl), wb, acc[j], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float xa = x[d][e >> 2][e & 3];
+        if constexpr (LNG) xa *= gv[d][e >> 2][e & 3];
+#pragma unroll
+        for (int j = 0; j < NPW; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, TL::get(w[d][j], e), acc[j], 0, 0, 0);
+      }
+    }
+  };
   // the input rows' LayerNorm statistics partials, loaded now and merged in
   // the epilogue (the kernel that wrote x left them)
   float2 lnp[LNG_PER];
   if (nt > 0) {
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) issue(d, d);
+    for (int d = 0; d < DEPTH_; ++d) issue(d, d);
   }
   if constexpr (LNG) {
     const int mrow = min((tid & 255) >> 4, a.M - 1), sub = tid & 15;
@@ -266,43 +303,17 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
     }
   }
   if (nt > 0) {
-    for (int i0 = 0; i0 < nt; i0 += DEPTH) {
+    if constexpr (ONESHOT) {
 #pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        if (i0 + d < nt) {
-          if constexpr (WT == W_BF16) {
-            // bf16 weights: the tile is one v_mfma_f32_16x16x32_bf16 B operand;
-            // x enters as three exact bf16 parts, so every product w * part is
-            // exact in f32 and the MFMA accumulates in f32: the f32 GEMV up to
-            // summation order (3 MFMAs per tile instead of 8 of 16x16x4 f32;
-            // measured ~10% faster, with half the error against a float64 sum)
-            float xs[8];
+      for (int d = 0; d < DEPTH_; ++d)
+        if (d < nt) consume(d);
+    } else {
+      for (int i0 = 0; i0 < nt; i0 += DEPTH_) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              xs[e] = x[d][e >> 2][e & 3];
-              if constexpr (LNG) xs[e] *= gv[d][e >> 2][e & 3];
-            }
-            u4v xh, xm, xl;
-            split3(xs, xh, xm, xl);
-#pragma unroll
-            for (int j = 0; j < NPW; ++j) {
-              const bf16x8 wb = as_bf16x8(w[d][j]);
-              acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xh), wb, acc[j], 0, 0, 0);
-              acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xm), wb, acc[j], 0, 0, 0);
-              acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xl), wb, acc[j], 0, 0, 0);
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-              float xa = x[d][e >> 2][e & 3];
-              if constexpr (LNG) xa *= gv[d][e >> 2][e & 3];
-#pragma unroll
-              for (int j = 0; j < NPW; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, TL::get(w[d][j], e), acc[j], 0, 0, 0);
-            }
-          }
+        for (int d = 0; d < DEPTH_; ++d) {
+          if (i0 + d < nt) consume(d);
+          issue(d, i0 + d + DEPTH_);
         }
-        issue(d, i0 + d + DEPTH);
       }
     }
   }
