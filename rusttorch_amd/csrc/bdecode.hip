@@ -86,8 +86,16 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
 template <int WT, int NPW, bool LNG>
 __device__ __forceinline__ void gemv_phase(const BgemvArgs& a, const BgemvPlan& pl, float* red, unsigned* last) {
   const int U = pl.groups * pl.S;
-  for (int u = blockIdx.x; u < U; u += BD_G)
-    bgc::bgemv_unit<WT, NPW, LNG, NW, true>(a, u / pl.S, u % pl.S, reinterpret_cast<float(*)[NPW][256]>(red), last);
+  // a wave's whole k-chunk in flight at once when it has at most 8 tiles
+  if (pl.ktc <= 8) {
+    for (int u = blockIdx.x; u < U; u += BD_G)
+      bgc::bgemv_unit<WT, NPW, LNG, NW, true, 8, true>(a, u / pl.S, u % pl.S,
+                                                       reinterpret_cast<float(*)[NPW][256]>(red), last);
+  } else {
+    for (int u = blockIdx.x; u < U; u += BD_G)
+      bgc::bgemv_unit<WT, NPW, LNG, NW, true>(a, u / pl.S, u % pl.S, reinterpret_cast<float(*)[NPW][256]>(red),
+                                              last);
+  }
 }
 
 template <int WT, bool LNG>

@@ -64,8 +64,14 @@ void launch_keys_to_tokens(hipStream_t s, int B, unsigned long long* keys, uint3
 void launch_reset_keys(hipStream_t s, int B, unsigned long long* keys);
 
 // Prefill GEMM on MFMA: C[M][N] = epi(A[M][K] * W[N][K]^T); C row stride ldc.
+// ws (ws_floats floats, may be null) holds split-k partial tiles: shapes with
+// too few output tiles to fill the GPU split k when it is large enough
+// (gemm_splitk_ws_floats), otherwise they run unsplit.
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
-                 long ldc, int M, int N, int K, int epi);
+                 long ldc, int M, int N, int K, int epi, float* ws = nullptr, size_t ws_floats = 0);
+// Workspace floats launch_gemm / launch_gemm_qkv use to split an M x N x K
+// GEMM over k (0: it runs unsplit).
+size_t gemm_splitk_ws_floats(int M, int N, int K);
 // Prefill: append k/v columns of qkv [S*T][3d] into the cache at past.. past+T.
 void launch_kv_append(hipStream_t s, const float* qkv, int S, int T, int past, KvDst kv);
 // Prefill c_attn: C = A W^T + bias with the k/v columns ([d, 3d)) of row
@@ -74,7 +80,8 @@ void launch_kv_append(hipStream_t s, const float* qkv, int S, int T, int past, K
 // Falls back to launch_gemm + launch_kv_append where the fused kernel does not
 // apply (f32 weights, K % 64 == 0, 16-byte aligned operands, more than 64 rows).
 void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
-                     long ldc, int M, int K, int S, int T, int past, KvDst kv);
+                     long ldc, int M, int K, int S, int T, int past, KvDst kv, float* ws = nullptr,
+                     size_t ws_floats = 0);
 // Prefill causal attention for S sequences of T new tokens at offset past.
 void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past, const float* kc, const float* vc,
                          int n_head, int n_pos, int d, float* out);

@@ -733,7 +733,8 @@ __device__ __forceinline__ void gl_step(int kt, int nk, float (&lds)[2][GBM * 16
 __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__ A, int lda,
                                                        const float* __restrict__ W, const float* __restrict__ bias,
                                                        float* __restrict__ C, long ldc, int M, int N, int K, int epi,
-                                                       int m_fast, KvDst kv, int kv_T, int kv_past) {
+                                                       int m_fast, KvDst kv, int kv_T, int kv_past, int ks,
+                                                       float* __restrict__ ws) {
   __shared__ __attribute__((aligned(16))) float st0[2][GBM * 16];
   __shared__ __attribute__((aligned(16))) float st1[2][GBM * 16];
   __shared__ __attribute__((aligned(16))) float st2[2][GBM * 16];
@@ -744,9 +745,13 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__
   // block order: with m_fast the row blocks of one W column block are
   // consecutive (W read once while A cycles through the cache), else the
   // column blocks of one A row block (A read once while W cycles)
+  // with ks > 1 the k range is split: block b handles tile b % (nmb * nnb)
+  // over k-split z = b / (nmb * nnb) and stores its raw partial tile to
+  // ws[z] (summed and finished by splitk_reduce_kernel)
   const int nmb = (M + GBM - 1) / GBM, nnb = (N + GBN - 1) / GBN;
-  const int bid = blockIdx.x;
+  const int bid = blockIdx.x % (nmb * nnb), z = blockIdx.x / (nmb * nnb);
   const int m0 = (m_fast ? bid % nmb : bid / nnb) * GBM, n0 = (m_fast ? bid / nmb : bid % nnb) * GBN;
+  const int nk = K / 16 / ks;  // k-tiles of this split, a multiple of GL_NS
 
   // this lane's load sources: groups 2*wave and 2*wave + 1 of A and of W
   const int lr = lane >> 2;
@@ -756,8 +761,8 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__
   for (int q = 0; q < 2; ++q) {
     const int row = (2 * wave + q) * 16 + lr;
     const int c = (lane & 3) ^ gl_swz(row);
-    asrc[q] = A + (size_t)min(m0 + row, M - 1) * lda + c * 4;
-    wsrc[q] = W + (size_t)min(n0 + row, N - 1) * K + c * 4;
+    asrc[q] = A + (size_t)min(m0 + row, M - 1) * lda + c * 4 + (size_t)z * nk * 16;
+    wsrc[q] = W + (size_t)min(n0 + row, N - 1) * K + c * 4 + (size_t)z * nk * 16;
   }
   auto issue = [&](int kt, float (&st)[2][GBM * 16]) {
 #pragma unroll
@@ -790,7 +795,6 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nk = K / 16;  // a multiple of GL_NS (K % 64 == 0)
   issue(0, st0);
   issue(1, st1);
   issue(2, st2);
@@ -801,6 +805,22 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__
     gl_step<3>(kt + 3, nk, st3, st2, asrc, wsrc, wave, aoff, woff, acc);
   }
 
+  if (ws != nullptr) {
+    float* wz = ws + (size_t)z * M * N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn + j * 32 + (lane & 31);
+        if (n >= N) continue;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (m < M) wz[(size_t)m * N + n] = acc[i][j][e];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -1041,33 +1061,104 @@ static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W,
   return true;
 }
 
+// Sum of the ks split-k partial tiles of gemm_lds_kernel (ws[z][m][n], in z
+// order) and the epilogue that kernel applies without a split (bias, gelu,
+// residual; with kv set, the k / v columns of c_attn go into the cache).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int ks, int M, int N,
+                                                            const float* __restrict__ bias, float* __restrict__ C,
+                                                            long ldc, int epi, KvDst kv, int kv_T, int kv_past) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)M * N) return;
+  const int m = (int)(i / N), n = (int)(i - (long)m * N);
+  float v = ws[i];
+  for (int z = 1; z < ks; ++z) v += ws[(size_t)z * M * N + i];
+  const float bv = bias ? bias[n] : 0.f;
+  if (kv.k != nullptr && n >= kv.d) {
+    const int which = n >= 2 * kv.d, cc = n - kv.d - which * kv.d;
+    const int sq = m / kv_T, t = m - sq * kv_T;
+    float* base = which ? kv.v : kv.k;
+    base[((size_t)sq * kv.n_head + (cc >> 6)) * kv.n_pos * 64 + (size_t)(kv_past + t) * 64 + (cc & 63)] = v + bv;
+    return;
+  }
+  float* cp = C + (size_t)m * ldc + n;
+  if (epi == EPI_BIAS) *cp = v + bv;
+  else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
+  else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
+  else *cp = v;
+}
+
+// k-splits of gemm_lds_kernel for an M x N x K GEMM: 1 when the output tiles
+// alone give enough workgroups (>= 192) or M < 128, else the smallest split
+// that gives >= 240 workgroups (each split a multiple of 4 k-tiles), or the
+// largest valid one up to 16. (Prefills of a few hundred rows otherwise run
+// their d-wide GEMMs on 32-48 of the 256 CUs.)
+int gemm_splitk_factor(int M, int N, int K) {
+  const int tiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+  if (M < 128 || tiles >= 192 || K % 64 != 0) return 1;
+  const int nk = K / 16;
+  int best = 1;
+  for (int s = 2; s <= 16; ++s) {
+    if (nk % (GL_NS * s) != 0) continue;
+    best = s;
+    if (tiles * s >= 240) break;
+  }
+  return best;
+}
+
+size_t gemm_splitk_ws_floats(int M, int N, int K) {
+  const int ks = gemm_splitk_factor(M, N, K);
+  return ks > 1 ? (size_t)ks * M * N : 0;
+}
+
+static bool gemm_lds_ok(const float* A, int lda, const void* W, int wtype, int K) {
+  return wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(W) & 15) == 0;
+}
+
+// gemm_lds_kernel, split over k when that fills the GPU and ws holds the
+// partial tiles (ws_floats of them), then the split-k reduction.
+static void launch_gemm_lds(hipStream_t s, const float* A, int lda, const float* W, const float* bias, float* C,
+                            long ldc, int M, int N, int K, int epi, KvDst kv, int kv_T, int kv_past, float* ws,
+                            size_t ws_floats) {
+  const int nb = ((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM);
+  int ks = gemm_splitk_factor(M, N, K);
+  if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
+  if (ks == 1) {
+    gemm_lds_kernel<<<nb, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, N > M ? 1 : 0, kv, kv_T, kv_past, 1,
+                                       nullptr);
+    return;
+  }
+  gemm_lds_kernel<<<nb * ks, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, N > M ? 1 : 0, kv, kv_T, kv_past,
+                                          ks, ws);
+  const long total = (long)M * N;
+  splitk_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(ws, ks, M, N, bias, C, ldc, epi, kv, kv_T,
+                                                                      kv_past);
+}
+
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
-                 long ldc, int M, int N, int K, int epi) {
+                 long ldc, int M, int N, int K, int epi, float* ws, size_t ws_floats) {
   if (launch_skinny(s, A, lda, W, wtype, bias, C, ldc, M, N, K, epi, SkinnyQkv{})) return;
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
-  if (wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
-      (reinterpret_cast<uintptr_t>(W) & 15) == 0)
+  if (gemm_lds_ok(A, lda, W, wtype, K))
     // (256 x 128 tiles with 3 stages, bounded to two waves per SIMD, were 2-4%
     // faster on the c4 shapes without an epilogue but made the c4 prefill
     // slower, 70.7k against 72.5k tokens/s; 3 stages at three waves per SIMD
     // and 2 stages at four were no faster than this kernel)
-    gemm_lds_kernel<<<grid.x * grid.y, 256, 0, s>>>(A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N,
-                                                    K, epi, N > M ? 1 : 0, KvDst{}, 1, 0);
+    launch_gemm_lds(s, A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, epi, KvDst{}, 1, 0, ws,
+                    ws_floats);
   else if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
   else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
 }
 
 void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
-                     long ldc, int M, int K, int S, int T, int past, KvDst kv) {
+                     long ldc, int M, int K, int S, int T, int past, KvDst kv, float* ws, size_t ws_floats) {
   const int N = 3 * kv.d;
-  if (M > 64 && wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
-      (reinterpret_cast<uintptr_t>(W) & 15) == 0 && kv.d == 64 * kv.n_head) {
-    const int nb = ((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM);
-    gemm_lds_kernel<<<nb, 256, 0, s>>>(A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, EPI_BIAS,
-                                       N > M ? 1 : 0, kv, T, past);
+  if (M > 64 && gemm_lds_ok(A, lda, W, wtype, K) && kv.d == 64 * kv.n_head) {
+    launch_gemm_lds(s, A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, EPI_BIAS, kv, T, past, ws,
+                    ws_floats);
     return;
   }
-  launch_gemm(s, A, lda, W, wtype, bias, C, ldc, M, N, K, EPI_BIAS);
+  launch_gemm(s, A, lda, W, wtype, bias, C, ldc, M, N, K, EPI_BIAS, ws, ws_floats);
   launch_kv_append(s, C, S, T, past, kv);
 }
 

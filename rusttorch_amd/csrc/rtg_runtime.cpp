@@ -150,6 +150,8 @@ struct rtg_cache {
   // work buffers, capacity in rows
   size_t rows_cap = 0;
   float *x = nullptr, *ln = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr;
+  float* ws = nullptr;  // split-k partial tiles of the prefill GEMMs
+  size_t ws_floats = 0;
   size_t logit_rows_cap = 0;
   float* logits = nullptr;
   // decode graph over the current buffers
@@ -173,11 +175,12 @@ struct rtg_cache {
 };
 
 static void free_work(rtg_cache* c) {
-  for (float** p : {&c->x, &c->ln, &c->qkv, &c->att, &c->h}) {
+  for (float** p : {&c->x, &c->ln, &c->qkv, &c->att, &c->h, &c->ws}) {
     if (*p) hipFree(*p);
     *p = nullptr;
   }
   c->rows_cap = 0;
+  c->ws_floats = 0;
 }
 
 static void destroy_graph(rtg_cache* c) {
@@ -198,6 +201,17 @@ static void ensure_rows(rtg_cache* c, size_t rows) {
   HIPX(hipMalloc(&c->qkv, cap * 3 * d * 4));
   HIPX(hipMalloc(&c->att, cap * d * 4));
   HIPX(hipMalloc(&c->h, cap * 4 * d * 4));
+  // the split-k workspace for the largest need of the four layer GEMMs at
+  // any row count up to cap (the split depends on the row blocks)
+  size_t ws = 0;
+  for (size_t r = 128; r < cap + 128; r += 128) {
+    const int M = (int)std::min(r, cap);
+    for (const auto& nk : {std::make_pair(3 * d, d), std::make_pair(d, d), std::make_pair(4 * d, d),
+                           std::make_pair(d, 4 * d)})
+      ws = std::max(ws, gemm_splitk_ws_floats(M, (int)nk.first, (int)nk.second));
+  }
+  if (ws) HIPX(hipMalloc(&c->ws, ws * 4));
+  c->ws_floats = ws;
   c->rows_cap = cap;
 }
 
@@ -263,12 +277,17 @@ static KvDst kv_layer(const rtg_cache* c, size_t l) {
 }
 
 // Activation buffers of one forward pass: x, ln [M][d], qkv [M][3d],
-// att [M][d], h [M][4d] and the logits rows.
+// att [M][d], h [M][4d], the logits rows and the GEMMs' split-k workspace
+// (ws_floats floats; null: the GEMMs run unsplit).
 struct Work {
   float *x, *ln, *qkv, *att, *h, *logits;
+  float* ws;
+  size_t ws_floats;
 };
 
-static Work cache_work(const rtg_cache* c) { return Work{c->x, c->ln, c->qkv, c->att, c->h, c->logits}; }
+static Work cache_work(const rtg_cache* c) {
+  return Work{c->x, c->ln, c->qkv, c->att, c->h, c->logits, c->ws, c->ws_floats};
+}
 
 // forward_cached body for S sequences x T new tokens (gpt2.rs:376-396) on the
 // MFMA prefill path, on the activation buffers w. ids_dev holds S*T ids;
@@ -285,12 +304,14 @@ static void enqueue_prefill(rtg_cache* c, const Work& w, const uint32_t* ids_dev
     const LayerW& L = m->layers[l];
     KvDst kv = kv_layer(c, l);
     launch_layernorm(s, w.x, L.ln1w, L.ln1b, eps, M, d, w.ln);
-    launch_gemm_qkv(s, w.ln, d, L.wqkv, m->wtype, L.bqkv, w.qkv, 3 * d, M, d, (int)S, (int)T, (int)past, kv);
+    launch_gemm_qkv(s, w.ln, d, L.wqkv, m->wtype, L.bqkv, w.qkv, 3 * d, M, d, (int)S, (int)T, (int)past, kv, w.ws,
+                    w.ws_floats);
     launch_attn_prefill(s, w.qkv, (int)S, (int)T, (int)past, kv.k, kv.v, kv.n_head, kv.n_pos, d, w.att);
-    launch_gemm(s, w.att, d, L.waproj, m->wtype, L.baproj, w.x, d, M, d, d, EPI_BIAS_RESID);
+    launch_gemm(s, w.att, d, L.waproj, m->wtype, L.baproj, w.x, d, M, d, d, EPI_BIAS_RESID, w.ws, w.ws_floats);
     launch_layernorm(s, w.x, L.ln2w, L.ln2b, eps, M, d, w.ln);
-    launch_gemm(s, w.ln, d, L.wfc, m->wtype, L.bfc, w.h, 4 * d, M, 4 * d, d, EPI_BIAS_GELU);
-    launch_gemm(s, w.h, 4 * d, L.wmproj, m->wtype, L.bmproj, w.x, d, M, d, 4 * d, EPI_BIAS_RESID);
+    launch_gemm(s, w.ln, d, L.wfc, m->wtype, L.bfc, w.h, 4 * d, M, 4 * d, d, EPI_BIAS_GELU, w.ws, w.ws_floats);
+    launch_gemm(s, w.h, 4 * d, L.wmproj, m->wtype, L.bmproj, w.x, d, M, d, 4 * d, EPI_BIAS_RESID, w.ws,
+                w.ws_floats);
   }
   launch_layernorm(s, w.x, m->lnfw, m->lnfb, eps, M, d, w.ln);
   if (logit_mode == 0) {
@@ -1227,6 +1248,8 @@ rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, 
     // output rows in full before they are read (the residual epilogues add
     // into x after the embedding has written it).
     Work w;
+    w.ws = nullptr;  // n <= 72 rows: no GEMM of the pass splits k
+    w.ws_floats = 0;
     w.x = sp;
     w.ln = w.x + pd;
     w.att = w.ln + pd;
