@@ -537,7 +537,7 @@ constexpr int GBM = 128, GBN = 128, GBK = 16, GPAD = 4;
 template <int WT>
 __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, int lda, const void* __restrict__ W,
                                                    const float* __restrict__ bias, float* __restrict__ C, long ldc,
-                                                   int M, int N, int K, int epi) {
+                                                   int M, int N, int K, int epi, int ks, float* __restrict__ ws) {
   __shared__ float As[2][GBK][GBM + GPAD];
   __shared__ float Ws[2][GBK][GBN + GPAD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -605,13 +605,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nk = (K + GBK - 1) / GBK;
-  gload(0);
+  // with ks > 1 (K a multiple of 16 * ks) workgroup z = blockIdx.z sums the
+  // k range [z K / ks, (z + 1) K / ks) and stores its raw tile to ws[z]
+  const int nk = ks > 1 ? K / ks / GBK : (K + GBK - 1) / GBK;
+  const int kbeg = ks > 1 ? (int)blockIdx.z * (K / ks) : 0;
+  gload(kbeg);
   sstore(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * GBK);
+    if (kt + 1 < nk) gload(kbeg + (kt + 1) * GBK);
 #pragma unroll
     for (int kk = 0; kk < GBK; kk += 2) {
       const int kr = kk + (lane >> 5);
@@ -629,6 +632,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
     __syncthreads();
   }
 
+  if (ws != nullptr) {
+    float* wz = ws + (size_t)blockIdx.z * M * N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn + j * 32 + (lane & 31);
+        if (n >= N) continue;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (m < M) wz[(size_t)m * N + n] = acc[i][j][e];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -1092,13 +1111,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // that gives >= 240 workgroups (each split a multiple of 4 k-tiles), or the
 // largest valid one up to 16. (Prefills of a few hundred rows otherwise run
 // their d-wide GEMMs on 32-48 of the 256 CUs.)
-int gemm_splitk_factor(int M, int N, int K) {
+// granule: k-tiles of 16 a split must hold a multiple of (GL_NS for
+// gemm_lds_kernel's stage ring, 1 for gemm_kernel).
+int gemm_splitk_factor(int M, int N, int K, int granule) {
   const int tiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-  if (M < 128 || tiles >= 192 || K % 64 != 0) return 1;
+  if (M < 128 || tiles >= 192 || K % (16 * granule) != 0) return 1;
   const int nk = K / 16;
   int best = 1;
   for (int s = 2; s <= 16; ++s) {
-    if (nk % (GL_NS * s) != 0) continue;
+    if (nk % (granule * s) != 0) continue;
     best = s;
     if (tiles * s >= 240) break;
   }
@@ -1106,7 +1127,9 @@ int gemm_splitk_factor(int M, int N, int K) {
 }
 
 size_t gemm_splitk_ws_floats(int M, int N, int K) {
-  const int ks = gemm_splitk_factor(M, N, K);
+  // the larger of the two kernels' needs (which one runs depends on the
+  // weight type and alignment)
+  const int ks = std::max(gemm_splitk_factor(M, N, K, GL_NS), gemm_splitk_factor(M, N, K, 1));
   return ks > 1 ? (size_t)ks * M * N : 0;
 }
 
@@ -1121,7 +1144,7 @@ static void launch_gemm_lds(hipStream_t s, const float* A, int lda, const float*
                             long ldc, int M, int N, int K, int epi, KvDst kv, int kv_T, int kv_past, float* ws,
                             size_t ws_floats) {
   const int nb = ((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM);
-  int ks = gemm_splitk_factor(M, N, K);
+  int ks = gemm_splitk_factor(M, N, K, GL_NS);
   if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
   if (ks == 1) {
     gemm_lds_kernel<<<nb, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, N > M ? 1 : 0, kv, kv_T, kv_past, 1,
@@ -1146,8 +1169,19 @@ void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtyp
     // and 2 stages at four were no faster than this kernel)
     launch_gemm_lds(s, A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, epi, KvDst{}, 1, 0, ws,
                     ws_floats);
-  else if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
-  else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi);
+  else {
+    int ks = gemm_splitk_factor(M, N, K, 1);
+    if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
+    grid.z = ks;
+    float* wsk = ks > 1 ? ws : nullptr;
+    if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, ks, wsk);
+    else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, ks, wsk);
+    if (ks > 1) {
+      const long total = (long)M * N;
+      splitk_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(ws, ks, M, N, bias, C, ldc, epi, KvDst{},
+                                                                          1, 0);
+    }
+  }
 }
 
 void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
