@@ -220,9 +220,13 @@ struct SkinnyQkv {
 };
 
 // Skinny MFMA GEMM (defined with the prefill GEMM below); false when the
-// shape does not suit it.
+// shape does not suit it. With a workspace (ws) it may split k; kv_pre set
+// (a prompt's c_attn) requires that split, whose reduction then writes the
+// k / v columns into the cache (false otherwise).
 static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias,
-                          float* C, long ldc, int M, int N, int K, int epi, const SkinnyQkv& qkv);
+                          float* C, long ldc, int M, int N, int K, int epi, const SkinnyQkv& qkv,
+                          float* ws = nullptr, size_t ws_floats = 0, KvDst kv_pre = KvDst{}, int kv_T = 1,
+                          int kv_past = 0);
 
 template <int BM, int WT, int R>
 __global__ __launch_bounds__(256) void gemv_kernel(const void* __restrict__ W, const float* __restrict__ bias,
@@ -907,13 +911,15 @@ template <int WT>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const float* __restrict__ A, int lda,
                                                           const void* __restrict__ W, const float* __restrict__ bias,
                                                           float* __restrict__ C, long ldc, int M, int N, int K,
-                                                          int epi, SkinnyQkv qkv) {
+                                                          int epi, SkinnyQkv qkv, int ks, float* __restrict__ ws) {
   __shared__ float red[4][32][33];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, hh = lane >> 5;
   const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
-  const int KW = K / 4, KH = KW / 2;
-  const int k0 = wave * KW + hh * KH;  // this lane's run: [k0, k0 + KH)
+  // with ks > 1 workgroup z = blockIdx.z takes the k range [z K / ks,
+  // (z + 1) K / ks) (a multiple of 64) and stores its raw tile to ws[z]
+  const int KZ = K / ks, KW = KZ / 4, KH = KW / 2;
+  const int k0 = (int)blockIdx.z * KZ + wave * KW + hh * KH;  // this lane's run: [k0, k0 + KH)
   const float* arow = A + (size_t)min(m0 + r, M - 1) * lda + k0;
   const size_t wrow = (size_t)min(n0 + r, N - 1) * K + k0;
   floatx16 acc;
@@ -951,6 +957,10 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const float* __restric
     const int m = m0 + mi, n = n0 + ni;
     if (m >= M || n >= N) continue;
     const float v = ((red[0][mi][ni] + red[1][mi][ni]) + red[2][mi][ni]) + red[3][mi][ni];
+    if (ws != nullptr) {
+      ws[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = v;
+      continue;
+    }
     const float bv = bias ? bias[n] : 0.f;
     if (qkv.q) {
       const int d = qkv.d;
@@ -1061,9 +1071,43 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny16_kernel(const float* __r
   }
 }
 
+// k-splits of gemm_skinny_kernel (rows M <= 64, 32 x 32 tiles): 1 when the
+// tiles give >= 192 workgroups, else the smallest split of K into multiples
+// of 64 giving >= 240, or the largest valid one up to 16.
+static int skinny_splitk_factor(int M, int N, int K) {
+  const int tiles = ((N + 31) / 32) * ((M + 31) / 32);
+  if (M > 64 || M <= 16 || tiles >= 192 || K % 64 != 0) return 1;
+  const int nk = K / 64;
+  int best = 1;
+  for (int sp = 2; sp <= 16; ++sp) {
+    if (nk % sp != 0) continue;
+    best = sp;
+    if (tiles * sp >= 240) break;
+  }
+  return best;
+}
+
+static void splitk_reduce(hipStream_t s, const float* ws, int ks, int M, int N, const float* bias, float* C, long ldc,
+                          int epi, KvDst kv, int kv_T, int kv_past);
+
 static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias,
-                          float* C, long ldc, int M, int N, int K, int epi, const SkinnyQkv& qkv) {
+                          float* C, long ldc, int M, int N, int K, int epi, const SkinnyQkv& qkv, float* ws,
+                          size_t ws_floats, KvDst kv_pre, int kv_T, int kv_past) {
   if (M > 64 || K % 64 != 0 || lda % 4 != 0) return false;
+  int ks = qkv.q == nullptr ? skinny_splitk_factor(M, N, K) : 1;
+  if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
+  if (ks > 1) {
+    // partial tiles, then the fixed-order sum with the epilogue (and, for a
+    // prompt's c_attn, its k / v columns written into the cache)
+    dim3 grid((N + 31) / 32, (M + 31) / 32, ks);
+    if (wtype == W_F32)
+      gemm_skinny_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv, ks, ws);
+    else
+      gemm_skinny_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv, ks, ws);
+    splitk_reduce(s, ws, ks, M, N, bias, C, ldc, epi, kv_pre, kv_T, kv_past);
+    return true;
+  }
+  if (kv_pre.k != nullptr) return false;  // the prompt's k / v columns need the separate append
   if (M <= 16) {
     // (8 waves with twice the loads in flight measured slower: each wave
     // instruction already touches 16 rows, the address units saturate)
@@ -1075,8 +1119,10 @@ static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W,
     return true;
   }
   dim3 grid((N + 31) / 32, (M + 31) / 32);
-  if (wtype == W_F32) gemm_skinny_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv);
-  else gemm_skinny_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv);
+  if (wtype == W_F32)
+    gemm_skinny_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv, 1, nullptr);
+  else
+    gemm_skinny_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, qkv, 1, nullptr);
   return true;
 }
 
@@ -1106,6 +1152,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   else *cp = v;
 }
 
+static void splitk_reduce(hipStream_t s, const float* ws, int ks, int M, int N, const float* bias, float* C, long ldc,
+                          int epi, KvDst kv, int kv_T, int kv_past) {
+  const long total = (long)M * N;
+  splitk_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(ws, ks, M, N, bias, C, ldc, epi, kv, kv_T,
+                                                                      kv_past);
+}
+
 // k-splits of gemm_lds_kernel for an M x N x K GEMM: 1 when the output tiles
 // alone give enough workgroups (>= 192) or M < 128, else the smallest split
 // that gives >= 240 workgroups (each split a multiple of 4 k-tiles), or the
@@ -1129,7 +1182,8 @@ int gemm_splitk_factor(int M, int N, int K, int granule) {
 size_t gemm_splitk_ws_floats(int M, int N, int K) {
   // the larger of the two kernels' needs (which one runs depends on the
   // weight type and alignment)
-  const int ks = std::max(gemm_splitk_factor(M, N, K, GL_NS), gemm_splitk_factor(M, N, K, 1));
+  const int ks = std::max(std::max(gemm_splitk_factor(M, N, K, GL_NS), gemm_splitk_factor(M, N, K, 1)),
+                          skinny_splitk_factor(M, N, K));
   return ks > 1 ? (size_t)ks * M * N : 0;
 }
 
@@ -1153,14 +1207,12 @@ static void launch_gemm_lds(hipStream_t s, const float* A, int lda, const float*
   }
   gemm_lds_kernel<<<nb * ks, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, N > M ? 1 : 0, kv, kv_T, kv_past,
                                           ks, ws);
-  const long total = (long)M * N;
-  splitk_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(ws, ks, M, N, bias, C, ldc, epi, kv, kv_T,
-                                                                      kv_past);
+  splitk_reduce(s, ws, ks, M, N, bias, C, ldc, epi, kv, kv_T, kv_past);
 }
 
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
                  long ldc, int M, int N, int K, int epi, float* ws, size_t ws_floats) {
-  if (launch_skinny(s, A, lda, W, wtype, bias, C, ldc, M, N, K, epi, SkinnyQkv{})) return;
+  if (launch_skinny(s, A, lda, W, wtype, bias, C, ldc, M, N, K, epi, SkinnyQkv{}, ws, ws_floats)) return;
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
   if (gemm_lds_ok(A, lda, W, wtype, K))
     // (256 x 128 tiles with 3 stages, bounded to two waves per SIMD, were 2-4%
@@ -1176,11 +1228,7 @@ void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtyp
     float* wsk = ks > 1 ? ws : nullptr;
     if (wtype == W_F32) gemm_kernel<W_F32><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, ks, wsk);
     else gemm_kernel<W_BF16><<<grid, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, ks, wsk);
-    if (ks > 1) {
-      const long total = (long)M * N;
-      splitk_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(ws, ks, M, N, bias, C, ldc, epi, KvDst{},
-                                                                          1, 0);
-    }
+    if (ks > 1) splitk_reduce(s, ws, ks, M, N, bias, C, ldc, epi, KvDst{}, 1, 0);
   }
 }
 
@@ -1192,6 +1240,10 @@ void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int 
                     ws_floats);
     return;
   }
+  // a prompt of at most 64 rows: the split skinny GEMM's reduction writes the
+  // k / v columns into the cache itself
+  if (launch_skinny(s, A, lda, W, wtype, bias, C, ldc, M, N, K, EPI_BIAS, SkinnyQkv{}, ws, ws_floats, kv, T, past))
+    return;
   launch_gemm(s, A, lda, W, wtype, bias, C, ldc, M, N, K, EPI_BIAS, ws, ws_floats);
   launch_kv_append(s, C, S, T, past, kv);
 }

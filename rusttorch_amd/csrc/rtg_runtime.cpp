@@ -204,7 +204,7 @@ static void ensure_rows(rtg_cache* c, size_t rows) {
   // the split-k workspace for the largest need of the four layer GEMMs at
   // any row count up to cap (the split depends on the row blocks)
   size_t ws = 0;
-  for (size_t r = 128; r < cap + 128; r += 128) {
+  for (size_t r = 32; r < cap + 128; r += (r < 128 ? 32 : 128)) {
     const int M = (int)std::min(r, cap);
     for (const auto& nk : {std::make_pair(3 * d, d), std::make_pair(d, d), std::make_pair(4 * d, d),
                            std::make_pair(d, 4 * d)})
@@ -1236,7 +1236,15 @@ rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, 
   // (the same alignment, so the same kernels as rtg_forward_cached run)
   const size_t d = model->cfg.n_embd, V = model->cfg.vocab_size;
   const size_t pd = align_up(n * d, 64), p3 = align_up(3 * n * d, 64), p4 = align_up(4 * n * d, 64);
-  const size_t need = 3 * pd + p3 + p4 + align_up(n * V, 64);
+  const size_t pv = align_up(n * V, 64);
+  // the split-k partial tiles the pass's GEMMs use at n rows (as much as the
+  // cache's own workspace would hold for them, so the same kernels run)
+  size_t pw = 0;
+  for (const auto& nk : {std::make_pair(3 * d, d), std::make_pair(d, d), std::make_pair(4 * d, d),
+                         std::make_pair(d, 4 * d)})
+    pw = std::max(pw, gemm_splitk_ws_floats((int)n, (int)nk.first, (int)nk.second));
+  pw = align_up(pw, 64);
+  const size_t need = 3 * pd + p3 + p4 + pv + pw;
   if (need > kScratchFloats)
     return err(fmt("rtg_forward_cached_noalloc: %zu new tokens need %zu bytes of scratch; it holds %zu", n,
                    need * 4, kScratchFloats * 4));
@@ -1248,14 +1256,14 @@ rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, 
     // output rows in full before they are read (the residual epilogues add
     // into x after the embedding has written it).
     Work w;
-    w.ws = nullptr;  // n <= 72 rows: no GEMM of the pass splits k
-    w.ws_floats = 0;
     w.x = sp;
     w.ln = w.x + pd;
     w.att = w.ln + pd;
     w.qkv = w.att + pd;
     w.h = w.qkv + p3;
     w.logits = w.h + p4;
+    w.ws = pw ? w.logits + pv : nullptr;
+    w.ws_floats = pw;
     HIPX(hipMemcpyAsync(cache->ids_in, ids, n * 4, hipMemcpyHostToDevice, cache->stream));
     enqueue_prefill(cache, w, cache->ids_in, 1, n, cache->len, 0);
     HIPX(hipGetLastError());
