@@ -1,10 +1,6 @@
 // Device side of decode attention for head dim 64 (one new token per
-// sequence, multi_head_attention_cached, gpt2.rs:772-834), shared by the
-// attention kernel of the batched step (kernels.hip) and by the persistent
-// batched step (bdecode.hip), plus the cross-lane helpers of both attention
-// paths. COH: q and the new token's K/V row were written earlier in the same
-// launch by other workgroups, so q, K and V are loaded device-scope (sc1) and
-// the output stored device-scope.
+// sequence, multi_head_attention_cached, gpt2.rs:772-834) of the batched step
+// (kernels.hip), plus cross-lane helpers.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -53,32 +49,16 @@ __device__ __forceinline__ float fexp_a(float x) { return __builtin_amdgcn_exp2f
 
 constexpr int AF_RG = 4;  // row groups of 4 rows per window
 
-typedef float af4v __attribute__((ext_vector_type(4)));
 
 // K/V rows of one window: row r0 + 4t + grp (clamped to len - 1), this lane's
-// 4 dims at dq. COH: device-scope 16-byte loads through buffer descriptors on
-// the head's K and V (byte offsets below 2 GiB).
-template <bool COH>
+// 4 dims at dq.
 __device__ __forceinline__ void af_load(const float* Kh, const float* Vh, int r0, int len, int grp, int dq,
                                         float4 (&k4)[AF_RG], float4 (&v4)[AF_RG]) {
-  __amdgpu_buffer_rsrc_t ks, vs;
-  if constexpr (COH) {
-    ks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Kh), (short)0, 0x7ffffff0, 0x00020000);
-    vs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Vh), (short)0, 0x7ffffff0, 0x00020000);
-  }
 #pragma unroll
   for (int t = 0; t < AF_RG; ++t) {
     const int r = min(r0 + 4 * t + grp, len - 1);
-    if constexpr (COH) {
-      const unsigned off = (unsigned)((r * 64 + dq) * 4);
-      const af4v a = __builtin_amdgcn_raw_buffer_load_b128(ks, off, 0, 16);
-      const af4v b = __builtin_amdgcn_raw_buffer_load_b128(vs, off, 0, 16);
-      k4[t] = make_float4(a.x, a.y, a.z, a.w);
-      v4[t] = make_float4(b.x, b.y, b.z, b.w);
-    } else {
-      k4[t] = *reinterpret_cast<const float4*>(Kh + (size_t)r * 64 + dq);
-      v4[t] = *reinterpret_cast<const float4*>(Vh + (size_t)r * 64 + dq);
-    }
+    k4[t] = *reinterpret_cast<const float4*>(Kh + (size_t)r * 64 + dq);
+    v4[t] = *reinterpret_cast<const float4*>(Vh + (size_t)r * 64 + dq);
   }
 }
 
@@ -119,7 +99,7 @@ __device__ __forceinline__ void af_window(const float4 (&k4)[AF_RG], const float
 // dims each, DPP row sums). The wave states (m, l, o) merge in LDS (wp,
 // [NWV][AD_ITEM]) in wave order; out[b][h*64 + d] = o / l. Every thread of the
 // workgroup calls it.
-template <int NWV, bool COH>
+template <int NWV>
 __device__ __forceinline__ void attn_item(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
                                           const float* __restrict__ vc, int H, int P, int len, int h, int b,
                                           float* __restrict__ out, int ldo, float (*wp)[AD_ITEM]) {
@@ -132,26 +112,16 @@ __device__ __forceinline__ void attn_item(const float* __restrict__ q, int ldq, 
   float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
   const int nwin = (len + WR - 1) / WR;
   if (wave < nwin) {
-    float4 q4;
-    const float* qp = q + (size_t)b * ldq + h * 64 + dq;
-    if constexpr (COH) {
-      float* qq = const_cast<float*>(qp);
-      q4 = make_float4(__hip_atomic_load(qq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                       __hip_atomic_load(qq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                       __hip_atomic_load(qq + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                       __hip_atomic_load(qq + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    } else {
-      q4 = *reinterpret_cast<const float4*>(qp);
-    }
+    const float4 q4 = *reinterpret_cast<const float4*>(q + (size_t)b * ldq + h * 64 + dq);
     float4 ka[AF_RG], va[AF_RG], kb[AF_RG], vb[AF_RG];
-    af_load<COH>(Kh, Vh, wave * WR, len, grp, dq, ka, va);
+    af_load(Kh, Vh, wave * WR, len, grp, dq, ka, va);
     for (int w = wave; w < nwin; w += 2 * NWV) {
       const int wn = w + NWV;
-      if (wn < nwin) af_load<COH>(Kh, Vh, wn * WR, len, grp, dq, kb, vb);
+      if (wn < nwin) af_load(Kh, Vh, wn * WR, len, grp, dq, kb, vb);
       af_window(ka, va, q4, w * WR, len, grp, m, lsum, o4);
       if (wn >= nwin) break;
       const int wn2 = wn + NWV;
-      if (wn2 < nwin) af_load<COH>(Kh, Vh, wn2 * WR, len, grp, dq, ka, va);
+      if (wn2 < nwin) af_load(Kh, Vh, wn2 * WR, len, grp, dq, ka, va);
       af_window(kb, vb, q4, wn * WR, len, grp, m, lsum, o4);
     }
     // sum over the 4 row groups
@@ -184,9 +154,7 @@ __device__ __forceinline__ void attn_item(const float* __restrict__ q, int ldq, 
       Ls += wp[w][1] * f;
       o += wp[w][2 + tid] * f;
     }
-    float* op = out + (size_t)b * ldo + h * 64 + tid;
-    if constexpr (COH) __hip_atomic_store(op, o / Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *op = o / Ls;
+    out[(size_t)b * ldo + h * 64 + tid] = o / Ls;
   }
   __syncthreads();  // wp is free again
 }

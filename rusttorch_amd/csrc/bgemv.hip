@@ -59,7 +59,7 @@ template <int WT, int NPW, bool LNG, int DEPTH, bool ONESHOT>
 __global__ __launch_bounds__(64 * BG_NW) void bgemv_kernel(BgemvArgs a) {
   __shared__ float red[BG_NW][NPW][256];
   __shared__ unsigned last;
-  bgc::bgemv_unit<WT, NPW, LNG, BG_NW, false, DEPTH, ONESHOT>(a, blockIdx.x, blockIdx.y, red, &last);
+  bgc::bgemv_unit<WT, NPW, LNG, BG_NW, DEPTH, ONESHOT>(a, blockIdx.x, blockIdx.y, red, &last);
 }
 
 // k-tiles a wave keeps in flight: its whole chunk at once when that fits

@@ -1,13 +1,6 @@
-// Device side of the batched decode GEMV (bgemv.hip) and of the persistent
-// batched decode step (bdecode.hip): the tile-ordered MFMA GEMV unit, its
-// epilogues and the LayerNorm statistics they carry. See bgemv.hip for the
-// tile layout and the work split.
-//
-// COH: the unit's inputs were written earlier in the same launch by other
-// workgroups (the persistent step). Their loads then go out device-scope
-// (sc1) and its outputs are stored device-scope, because a plain load may be
-// served from a stale line of this CU's caches; weights and the other
-// per-model constants are read plainly either way.
+// Device side of the batched decode GEMV (bgemv.hip): the tile-ordered MFMA
+// GEMV unit, its epilogues and the LayerNorm statistics they carry. See
+// bgemv.hip for the tile layout and the work split.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -53,35 +46,6 @@ __device__ __forceinline__ void split3(const float (&x)[8], u4v& hi, u4v& mid, u
 }
 __device__ __forceinline__ bf16x8 as_bf16x8(const u4v& v) { return __builtin_bit_cast(bf16x8, v); }
 
-template <bool COH>
-__device__ __forceinline__ float ld1(const float* p) {
-  if constexpr (COH) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else return *p;
-}
-template <bool COH>
-__device__ __forceinline__ void st1(float* p, float v) {
-  if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else *p = v;
-}
-template <bool COH>
-__device__ __forceinline__ float2 ld2(const float* p) {
-  if constexpr (COH) {
-    const u64 u = __hip_atomic_load(reinterpret_cast<u64*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    return make_float2(__uint_as_float((unsigned)u), __uint_as_float((unsigned)(u >> 32)));
-  } else {
-    return *reinterpret_cast<const float2*>(p);
-  }
-}
-// 16-byte device-scope load through a buffer descriptor (sc1 cache policy);
-// byte offsets stay below 2 GiB of the descriptor's base.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0, 0x00020000);
-}
-__device__ __forceinline__ f4v ld4_sc1(__amdgpu_buffer_rsrc_t rs, unsigned byte_off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, 16);
-}
-
 __device__ __forceinline__ float gelu_new_b(float x) {
   const float sqrt_2_pi = 0.7978845608028654f;  // gpt2.rs:837-847, the reference's association
   float inner = sqrt_2_pi * (x + 0.044715f * x * x * x);
@@ -108,7 +72,6 @@ struct Tile<W_BF16> {
 };
 
 // Applies the epilogue to v (row m, output n) and returns the value written.
-template <bool COH>
 __device__ __forceinline__ float store_out(const BgemvArgs& a, int m, int n, float v) {
   const float bv = a.bias ? a.bias[n] : 0.f;
   if (a.qkv.q) {
@@ -116,13 +79,13 @@ __device__ __forceinline__ float store_out(const BgemvArgs& a, int m, int n, flo
     // *pos_dev (LayerKVCache::append, gpt2.rs:500-514)
     const int d = a.qkv.d;
     if (n < d) {
-      st1<COH>(a.qkv.q + (size_t)m * a.qkv.ldq + n, v + bv);
+      a.qkv.q[(size_t)m * a.qkv.ldq + n] = v + bv;
     } else {
       const int cc = n - (n < 2 * d ? d : 2 * d);
       const int hd = d / a.qkv.kv.n_head;
       const int h = cc / hd, dd = cc - h * hd;
       float* base = n < 2 * d ? a.qkv.kv.k : a.qkv.kv.v;
-      st1<COH>(base + (((size_t)m * a.qkv.kv.n_head + h) * a.qkv.kv.n_pos + *a.qkv.pos_dev) * hd + dd, v + bv);
+      base[(((size_t)m * a.qkv.kv.n_head + h) * a.qkv.kv.n_pos + *a.qkv.pos_dev) * hd + dd] = v + bv;
     }
     return v + bv;
   }
@@ -130,9 +93,9 @@ __device__ __forceinline__ float store_out(const BgemvArgs& a, int m, int n, flo
   float y;
   if (a.epi == EPI_BIAS) y = v + bv;
   else if (a.epi == EPI_BIAS_GELU) y = gelu_new_b(v + bv);
-  else if (a.epi == EPI_BIAS_RESID) y = ld1<COH>(cp) + (v + bv);
+  else if (a.epi == EPI_BIAS_RESID) y = *cp + (v + bv);
   else y = v;
-  st1<COH>(cp, y);
+  *cp = y;
   return y;
 }
 
@@ -147,7 +110,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 // columns it wrote, stored to stats_part[g][m] for the GEMV that reads x
 // next. y[j] are the values thread tid (< 256) wrote (valid[j] false for
 // columns past N or rows past M).
-template <int NPW, bool COH>
+template <int NPW>
 __device__ __forceinline__ void row_stats_partial(const BgemvArgs& a, int g, const float (&y)[NPW],
                                                   const bool (&valid)[NPW]) {
   const int tid = threadIdx.x, m = tid >> 4;
@@ -168,8 +131,8 @@ __device__ __forceinline__ void row_stats_partial(const BgemvArgs& a, int g, con
   }
   m2 = row16_sum(m2);
   if ((tid & 15) == 0 && m < a.M) {
-    st1<COH>(a.stats_part + ((size_t)g * 16 + m) * 2, mean);
-    st1<COH>(a.stats_part + ((size_t)g * 16 + m) * 2 + 1, m2);
+    a.stats_part[((size_t)g * 16 + m) * 2] = mean;
+    a.stats_part[((size_t)g * 16 + m) * 2 + 1] = m2;
   }
 }
 
@@ -208,7 +171,7 @@ __device__ __forceinline__ void row_stats_merge(const BgemvArgs& a, const float2
 // DEPTH_ k-tiles of a wave are in flight at once: a ring refilled as tiles
 // are consumed, or, with ONESHOT (the caller guarantees ktc <= DEPTH_), the
 // whole chunk loaded at once and consumed without refills.
-template <int WT, int NPW, bool LNG, int NW, bool COH, int DEPTH_ = DEPTH, bool ONESHOT = false>
+template <int WT, int NPW, bool LNG, int NW, int DEPTH_ = DEPTH, bool ONESHOT = false>
 __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, float (*red)[NPW][256],
                                            unsigned* last) {
   typedef Tile<WT> TL;
@@ -229,9 +192,6 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
   }
   const int xr = min(r, a.M - 1);
   const float* xrow = a.X + (size_t)xr * a.ldx + t0 * TK + q * E;
-  const unsigned xoff = (unsigned)(((size_t)xr * a.ldx + t0 * TK + q * E) * 4);
-  __amdgpu_buffer_rsrc_t xrs;
-  if constexpr (COH) xrs = rsrc_of(a.X);
   const float* grow = a.ln_g + t0 * TK + q * E;  // LayerNorm gain at the same k (LNG)
   floatx4 acc[NPW];
 #pragma unroll
@@ -248,8 +208,7 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
     for (int j = 0; j < NPW; ++j) w[slot][j] = __builtin_nontemporal_load(wp[j] + (size_t)ti * 64);
 #pragma unroll
     for (int h = 0; h < E / 4; ++h) {
-      if constexpr (COH) x[slot][h] = ld4_sc1(xrs, xoff + (unsigned)(ti * TK + 4 * h) * 4);
-      else x[slot][h] = *reinterpret_cast<const f4v*>(xrow + ti * TK + 4 * h);
+      x[slot][h] = *reinterpret_cast<const f4v*>(xrow + ti * TK + 4 * h);
       if constexpr (LNG) gv[slot][h] = *reinterpret_cast<const f4v*>(grow + ti * TK + 4 * h);
     }
   };
@@ -299,7 +258,7 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
 #pragma unroll
     for (int i = 0; i < LNG_PER; ++i) {
       const int gg = min(sub + 16 * i, a.ln_groups - 1);
-      lnp[i] = ld2<COH>(a.ln_part + ((size_t)gg * 16 + mrow) * 2);
+      lnp[i] = *reinterpret_cast<const float2*>(a.ln_part + ((size_t)gg * 16 + mrow) * 2);
     }
   }
   if (nt > 0) {
@@ -395,14 +354,14 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
     if (valid[j]) {
       float t = v[j];
       if constexpr (LNG) t = inv_std * (t - mean * a.ln_s[n]);
-      y[j] = store_out<COH>(a, m, n, t);
+      y[j] = store_out(a, m, n, t);
       if (a.keys) {
         const u64 k = argmax_key(y[j], (uint32_t)n);
         best = k > best ? k : best;
       }
     }
   }
-  if (a.stats_part) row_stats_partial<NPW, COH>(a, g, y, valid);
+  if (a.stats_part) row_stats_partial<NPW>(a, g, y, valid);
   if (a.keys) {
     // greedy argmax of the LM head: the row's best key over this unit, then
     // one device-scope atomic max per row

@@ -426,7 +426,7 @@ __global__ __launch_bounds__(64 * NWV) void attn_decode_fused_kernel(const float
                                                                     const int* __restrict__ pos_dev,
                                                                     float* __restrict__ out, int ldo) {
   __shared__ float wp[NWV][AD_ITEM];
-  attn_item<NWV, false>(q, ldq, kc, vc, H, P, *pos_dev + 1, blockIdx.x, blockIdx.y, out, ldo, wp);
+  attn_item<NWV>(q, ldq, kc, vc, H, P, *pos_dev + 1, blockIdx.x, blockIdx.y, out, ldo, wp);
 }
 
 void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc, int n_head,

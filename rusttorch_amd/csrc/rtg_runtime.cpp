@@ -19,7 +19,6 @@
 
 #include "../../include/rtgpu.h"
 #include "decode_persistent.h"
-#include "bdecode.h"
 #include "bgemv.h"
 #include "kernels.h"
 #include "safetensors_reader.h"
@@ -98,11 +97,7 @@ struct BatchedWeights {
   const void* lm = nullptr;  // tiled wte (the tied LM head)
   const float *sl = nullptr, *cl = nullptr;  // ln_f into the LM head
   BgemvPlan pq{}, pp{}, pf{}, pm{}, pl{};    // c_attn, attn c_proj, c_fc, mlp c_proj, LM head
-  // the persistent batched step (bdecode.h): its layer table and work split
-  BdLayer* bd_layers = nullptr;  // device [L]
-  BdPlans bd_plans{};
   ~BatchedWeights() {
-    if (bd_layers) hipFree(bd_layers);
     if (arena) hipFree(arena);
   }
 };
@@ -164,14 +159,6 @@ struct rtg_cache {
   float* bg_part = nullptr;
   unsigned* bg_cnt = nullptr;
   float* bg_spart = nullptr;
-  // persistent batched step (bdecode.h): barrier flags, error word, arrival
-  // counter; bd_bar_base = flag value reached so far
-  bool bd = false;
-  unsigned* bd_bar = nullptr;
-  unsigned* bd_err = nullptr;
-  unsigned* bd_done = nullptr;
-  unsigned bd_bar_base = 0;
-  unsigned long long* bd_trace = nullptr;  // RTG_TRACE_FILE: per-phase clock of workgroup 0
 };
 
 static void free_work(rtg_cache* c) {
@@ -386,19 +373,6 @@ static const BatchedWeights* ensure_batched(const rtg_model* mc) {
   bw->pf = bgemv_plan(4 * d, d, wt);
   bw->pm = bgemv_plan(d, 4 * d, wt);
   bw->pl = bgemv_plan(V, d, wt);
-  bw->bd_plans.pq = bd_plan(3 * d, d, wt);
-  bw->bd_plans.pp = bd_plan(d, d, wt);
-  bw->bd_plans.pf = bd_plan(4 * d, d, wt);
-  bw->bd_plans.pm = bd_plan(d, 4 * d, wt);
-  bw->bd_plans.pl = bd_plan(V, d, wt);
-  std::vector<BdLayer> bl(L);
-  for (int l = 0; l < L; ++l) {
-    const LayerW& W = m->layers[l];
-    const BatchedWeights::Layer& T = bw->layers[l];
-    bl[l] = BdLayer{T.qkv, T.proj, T.fc, T.mproj, T.cq, T.sq, T.cf, T.sf, W.ln1w, W.ln2w, W.baproj, W.bmproj};
-  }
-  HIPX(hipMalloc(&bw->bd_layers, sizeof(BdLayer) * std::max(L, 1)));
-  HIPX(hipMemcpy(bw->bd_layers, bl.data(), sizeof(BdLayer) * L, hipMemcpyHostToDevice));
   m->bw = std::move(bw);
   return m->bw.get();
 }
@@ -418,134 +392,11 @@ static void ensure_bg_work(rtg_cache* c, const BatchedWeights* bw) {
   HIPX(hipStreamSynchronize(c->stream));
 }
 
-// The persistent batched step (opt-in, RTG_BDECODE=1: measured slower than
-// the captured graph of per-op kernels, each phase costing about what a
-// kernel launch does) needs one workgroup per CU of a 256-CU device and
-// head_dim 64.
-static bool bd_ok(const rtg_model* m) {
-  const char* on = getenv("RTG_BDECODE");
-  if (!on || on[0] != '1') return false;
-  if (m->cfg.n_embd % 64 != 0 || m->cfg.n_head * 64 != m->cfg.n_embd) return false;
-  int dev = 0, cus = 0, coop = 0;
-  hipGetDevice(&dev);
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
-  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess) return false;
-  return cus == BD_G && coop != 0;
-}
-
 // Prepares the decode step of a cache without a batch-1 persistent state
-// (before any capture): the persistent batched step where it applies, else
-// the captured graph of per-op kernels; both need the batched weights.
+// (before any capture): the batched weights and the step's workspace.
 static void prepare_decode(rtg_cache* c) {
   if (c->pstate || !batched_ok(c->m, c->batch)) return;
-  const BatchedWeights* bw = ensure_batched(c->m);
-  if (!c->bd && bd_ok(c->m)) {
-    // split-k partials / counters and statistics partials sized for both
-    // sets of plans; barrier flags, error word and arrival counter
-    const size_t part = std::max(bd_part_floats(bw->bd_plans), (size_t)1);
-    const size_t groups = bd_groups(bw->bd_plans);
-    ensure_bg_work(c, bw);
-    float* p2 = nullptr;
-    unsigned* c2 = nullptr;
-    float* s2 = nullptr;
-    HIPX(hipMalloc(&p2, part * 4));
-    HIPX(hipMalloc(&c2, groups * 4));
-    HIPX(hipMalloc(&s2, groups * 16 * 2 * 4));
-    hipFree(c->bg_part);
-    hipFree(c->bg_cnt);
-    hipFree(c->bg_spart);
-    c->bg_part = p2;
-    c->bg_cnt = c2;
-    c->bg_spart = s2;
-    HIPX(hipMalloc(&c->bd_bar, BD_G * 128));
-    HIPX(hipMalloc(&c->bd_err, 256));
-    HIPX(hipMalloc(&c->bd_done, 256));
-    HIPX(hipMemsetAsync(c->bg_cnt, 0, groups * 4, c->stream));
-    HIPX(hipMemsetAsync(c->bd_bar, 0, BD_G * 128, c->stream));
-    HIPX(hipMemsetAsync(c->bd_err, 0, 256, c->stream));
-    HIPX(hipMemsetAsync(c->bd_done, 0, 256, c->stream));
-    HIPX(hipStreamSynchronize(c->stream));
-    c->bd_bar_base = 0;
-    if (getenv("RTG_TRACE_FILE")) {
-      const size_t n = (size_t)bd_barriers((int)c->m->layers.size()) + 2;
-      HIPX(hipMalloc(&c->bd_trace, n * 8));
-      HIPX(hipMemset(c->bd_trace, 0, n * 8));
-    }
-    c->bd = true;
-    destroy_graph(c);
-    return;
-  }
-  ensure_bg_work(c, bw);
-}
-
-// One step of the persistent batched decode (reads token_dev / pos_dev,
-// writes the logits, the argmax tokens and ids, advances pos and step).
-static void enqueue_bdecode(rtg_cache* c) {
-  const rtg_model* m = c->m;
-  const BatchedWeights* bw = m->bw.get();
-  BdParams p{};
-  p.layers = bw->bd_layers;
-  p.L = (int)m->layers.size();
-  p.B = (int)c->batch;
-  p.d = (int)m->cfg.n_embd;
-  p.V = (int)m->cfg.vocab_size;
-  p.H = (int)m->cfg.n_head;
-  p.P = (int)m->cfg.n_positions;
-  p.wtype = m->wtype;
-  p.eps = m->cfg.layer_norm_epsilon;
-  p.wte = m->wte;
-  p.wpe = m->wpe;
-  p.lm = bw->lm;
-  p.sl = bw->sl;
-  p.cl = bw->cl;
-  p.lnfw = m->lnfw;
-  p.kc = c->k;
-  p.vc = c->v;
-  p.kv_layer = (long)c->layer_stride;
-  p.x = c->x;
-  p.qkv = c->qkv;
-  p.att = c->att;
-  p.h = c->h;
-  p.logits = c->logits;
-  p.spart = c->bg_spart;
-  p.part = c->bg_part;
-  p.cnt = c->bg_cnt;
-  p.bar = c->bd_bar;
-  p.bar_base = c->bd_bar_base;
-  p.err = c->bd_err;
-  p.token = c->token_dev;
-  p.pos = c->pos_dev;
-  p.ids = c->ids_dev;
-  p.step = c->step_dev;
-  p.ld_ids = (int)m->cfg.n_positions;
-  p.keys = c->keys;
-  p.done = c->bd_done;
-  p.plan = bw->bd_plans;
-  p.trace = c->bd_trace;
-  HIPX(launch_bdecode(p, c->stream));
-  c->bd_bar_base += (unsigned)bd_barriers(p.L);
-}
-
-// Turns a timed-out wait of the persistent batched step into an error; with
-// RTG_TRACE_FILE set, writes the last step's per-phase clock (workgroup 0,
-// 100 MHz ticks: start, after each grid barrier, end of the LM head).
-static void check_bd(rtg_cache* c) {
-  if (!c->bd) return;
-  if (c->bd_trace) {
-    const size_t n = (size_t)bd_barriers((int)c->m->layers.size()) + 2;
-    std::vector<unsigned long long> h(n);
-    HIPX(hipMemcpy(h.data(), c->bd_trace, n * 8, hipMemcpyDeviceToHost));
-    if (FILE* f = fopen(getenv("RTG_TRACE_FILE"), "w")) {
-      for (size_t i = 0; i < n; ++i) fprintf(f, "%llu\n", h[i]);
-      fclose(f);
-    }
-  }
-  unsigned e = 0;
-  HIPX(hipMemcpy(&e, c->bd_err, 4, hipMemcpyDeviceToHost));
-  if (e) {
-    HIPX(hipMemset(c->bd_err, 0, 4));
-    throw HipError{fmt("persistent batched decode step timed out at a grid barrier (code %u)", e)};
-  }
+  ensure_bg_work(c, ensure_batched(c->m));
 }
 
 // One decode step for B sequences: per layer four tile-ordered GEMVs with
@@ -640,9 +491,6 @@ static void enqueue_decode_step(rtg_cache* c) {
   const int P = (int)m->cfg.n_positions;
   if (c->pstate) {
     HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/false));
-  } else if (c->bd) {
-    enqueue_bdecode(c);
-    return;  // the step finishes itself
   } else if (c->bg_part) {
     enqueue_decode_step_batched(c);
   } else {
@@ -722,7 +570,6 @@ static void forward_cached_impl(rtg_cache* c, const uint32_t* ids, size_t n, flo
   }
   if (logits_out) HIPX(hipMemcpyAsync(logits_out, c->logits, B * n * V * 4, hipMemcpyDeviceToHost, c->stream));
   HIPX(hipStreamSynchronize(c->stream));
-  check_bd(c);
   c->len += n;
 }
 
@@ -800,7 +647,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   // RTG_NO_GRAPH=1 does the same for the batched step's kernels (for
   // per-kernel profiling; same results).
   const char* ng = getenv("RTG_NO_GRAPH");
-  if (c->pstate || c->bd || (ng && ng[0] == '1')) {
+  if (c->pstate || (ng && ng[0] == '1')) {
     for (size_t i = 1; i < steps; ++i) {
       enqueue_decode_step(c);
       sample(c->logits);
@@ -840,7 +687,6 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   std::vector<uint32_t> gen(B * P);
   HIPX(hipMemcpyAsync(gen.data(), c->ids_dev, B * P * 4, hipMemcpyDeviceToHost, s));
   HIPX(hipStreamSynchronize(s));
-  check_bd(c);
   if (c->pstate) {
     persistent_dump_trace(c->pstate);
     unsigned e = 0;
@@ -1180,8 +1026,7 @@ void rtg_cache_destroy(rtg_cache* c) {
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
                   (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->logits,
-                  (void*)c->bg_part, (void*)c->bg_cnt, (void*)c->bg_spart, (void*)c->bd_bar, (void*)c->bd_err,
-                  (void*)c->bd_done, (void*)c->bd_trace})
+                  (void*)c->bg_part, (void*)c->bg_cnt, (void*)c->bg_spart})
     if (p) hipFree(p);
   for (auto e : c->ev)
     if (e) hipEventDestroy(e);

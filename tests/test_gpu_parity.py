@@ -404,25 +404,6 @@ def test_small_batched_decode_logits(O):
     _batched_step_logits(O, sd, sh, m, 4, 20, 3, 470, "small b=4")
 
 
-def test_persistent_batched_step_matches_oracle(O, monkeypatch):
-    """The opt-in persistent batched step (RTG_BDECODE=1: the whole decode
-    step in one cooperative launch, grid barriers between phases): its
-    logits at GPT-2 small b=4 against the oracle, and its greedy ids equal to
-    the default (graph) path's."""
-    sd, sh, _ = gpu_model("small")
-    monkeypatch.setenv("RTG_BDECODE", "1")
-    m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
-    _batched_step_logits(O, sd, sh, m, 4, 20, 3, 490, "small b=4 persistent")
-    prompts = np.stack([synth.make_tokens(40, sh.vocab_size, stream=495 + b) for b in range(3)])
-    out = m.generate_cached_batched(prompts, 24)
-    m.close()
-    monkeypatch.delenv("RTG_BDECODE")
-    m2 = Gpt2Model.from_state_dict(sd, cfg_of(sh))
-    ref = m2.generate_cached_batched(prompts, 24)
-    m2.close()
-    assert out.tolist() == ref.tolist()
-
-
 def test_batched_step_odd_batch_and_batch_one(O, monkeypatch):
     """The tile-ordered batched step with partly used MFMA rows: 13 sequences
     (logits against the oracle), and batch 1 with the persistent kernel
