@@ -524,7 +524,10 @@ __device__ __forceinline__ int slot_of(int i) {
 // the same line requests as polling a per-producer flag would, and saves
 // the flag's extra round trip. The NW = ceil(NMAX / 192) words of a lane in
 // a chunk of NMAX words are in flight together, so an exchange of n <= NMAX
-// words costs one polling round trip; longer ones take n / NMAX. With SCALE,
+// words costs one polling round trip; longer ones take n / NMAX. A stale
+// word is re-read as soon as its round returns (c1: 227.3 µs per token
+// against 228.2 with a 64-clock sleep between rounds, 232.7 with 512; two
+// staggered rounds in flight per word: 252 µs). With SCALE,
 // dst2[i] = word * g[i] as well (the LayerNorm gain applied to a GEMV input
 // whose LayerNorm is folded).
 template <int RPW, int SW, int NMAX, bool SCALE = false>
@@ -558,7 +561,6 @@ __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, 
         raise_err(err, 1u);
         break;
       }
-      __builtin_amdgcn_s_sleep(1);
 #pragma unroll
       for (int k = 0; k < NW; ++k) {
         const int i = base + gl + k * NG;
@@ -736,7 +738,6 @@ __device__ __forceinline__ void poll_words(const u64* src, const int (&idx)[NW],
       raise_err(err, 1u);
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int k = 0; k < NW; ++k)
       if (k < n && (unsigned)(w[k] >> 32) != tag) w[k] = tload(src + idx[k]);
