@@ -587,8 +587,30 @@ int orc_forward_cached(const orc_model* m, orc_cache* c, const uint32_t* ids, si
 
 /* generate_cached with temperature <= 0, gpt2.rs:405-441. The prefill token
  * is pushed even when max_new == 0, as in the reference. */
+/* Top-1 minus top-2 value of a logits row (NaN skipped; a tie at the top gives
+ * 0): the margin by which the greedy choice of that row won. Diagnostic only,
+ * for telling a near tie from a wrong logit when greedy ids differ. */
+float orc_top2_gap(const float* data, size_t n) {
+  float b1 = -INFINITY, b2 = -INFINITY;
+  for (size_t i = 0; i < n; ++i) {
+    const float v = data[i];
+    if (v > b1) {
+      b2 = b1;
+      b1 = v;
+    } else if (v > b2) {
+      b2 = v;
+    }
+  }
+  return (b1 > -INFINITY && b2 > -INFINITY) ? b1 - b2 : INFINITY;
+}
+
 int orc_generate_cached(const orc_model* m, const uint32_t* prompt, size_t n, size_t max_new, uint32_t* out,
                         char* err) {
+  return orc_generate_cached_gaps(m, prompt, n, max_new, out, NULL, err);
+}
+
+int orc_generate_cached_gaps(const orc_model* m, const uint32_t* prompt, size_t n, size_t max_new, uint32_t* out,
+                             float* gaps, char* err) {
   size_t V = m->cfg.vocab_size;
   orc_cache* c = orc_cache_new(m);
   float* logits = (float*)malloc((n ? n : 1) * V * sizeof(float));
@@ -597,10 +619,12 @@ int orc_generate_cached(const orc_model* m, const uint32_t* prompt, size_t n, si
     memcpy(out, prompt, n * sizeof(uint32_t));
     size_t len = n;
     out[len++] = orc_argmax(logits + (n - 1) * V, V);
+    if (gaps) gaps[0] = orc_top2_gap(logits + (n - 1) * V, V);
     for (size_t s = 1; s < max_new; ++s) {
       uint32_t last = out[len - 1];
       rc = orc_forward_cached(m, c, &last, 1, logits, err);
       if (rc != 0) break;
+      if (gaps) gaps[s] = orc_top2_gap(logits, V);
       out[len++] = orc_argmax(logits, V);
     }
   }

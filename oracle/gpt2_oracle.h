@@ -70,6 +70,11 @@ int orc_forward_cached(const orc_model* m, orc_cache* c, const uint32_t* ids, si
 int orc_generate_cached(const orc_model* m, const uint32_t* prompt, size_t n, size_t max_new, uint32_t* out,
                         char* err);
 int orc_generate(const orc_model* m, const uint32_t* prompt, size_t n, size_t max_new, uint32_t* out, char* err);
+/* generate_cached that also writes, for each greedy step s, the top-1 minus
+ * top-2 logit of the row it chose from into gaps[s] (max(1, max_new) floats). */
+int orc_generate_cached_gaps(const orc_model* m, const uint32_t* prompt, size_t n, size_t max_new, uint32_t* out,
+                             float* gaps, char* err);
+float orc_top2_gap(const float* data, size_t n);
 
 #ifdef __cplusplus
 }

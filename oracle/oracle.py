@@ -75,6 +75,9 @@ def lib() -> C.CDLL:
         L.orc_forward_cached.argtypes = [vp, vp, vp, sz, vp, C.c_char_p]
         L.orc_generate_cached.argtypes = [vp, vp, sz, sz, vp, C.c_char_p]
         L.orc_generate.argtypes = [vp, vp, sz, sz, vp, C.c_char_p]
+        L.orc_generate_cached_gaps.argtypes = [vp, vp, sz, sz, vp, vp, C.c_char_p]
+        L.orc_top2_gap.argtypes = [vp, sz]
+        L.orc_top2_gap.restype = C.c_float
         _lib = L
     return _lib
 
@@ -148,6 +151,12 @@ def gelu_new(x) -> np.ndarray:
     out = np.empty_like(x)
     lib().orc_gelu_new(_p(x), x.size, _p(out))
     return out
+
+
+def top2_gap(x) -> float:
+    """Top-1 minus top-2 value of a logits row (inf with fewer than two)."""
+    a = _f32(x)
+    return float(lib().orc_top2_gap(_p(a), a.size))
 
 
 def argmax(x) -> int:
@@ -255,13 +264,16 @@ class OracleModel:
             raise OracleError(e.value.decode())
         return out[: i.size]
 
-    def generate_cached(self, ids, max_new) -> list:
+    def generate_cached(self, ids, max_new, gaps=False):
+        """Greedy ids; with gaps=True also the top-1 minus top-2 logit of
+        every greedy step's row, as (ids, gaps)."""
         i = _u32(ids)
         out = np.empty(i.size + max(1, max_new), dtype=np.uint32)
+        g = np.full(max(1, max_new), np.nan, dtype=np.float32)
         e = _err()
-        if lib().orc_generate_cached(self._h, _p(i), i.size, max_new, _p(out), e) != 0:
+        if lib().orc_generate_cached_gaps(self._h, _p(i), i.size, max_new, _p(out), _p(g), e) != 0:
             raise OracleError(e.value.decode())
-        return out.tolist()
+        return (out.tolist(), g) if gaps else out.tolist()
 
     def generate(self, ids, max_new) -> list:
         i = _u32(ids)

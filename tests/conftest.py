@@ -28,3 +28,15 @@ def oracle_lib():
     from oracle import oracle
     oracle.build()
     return oracle
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The greedy near-tie log: per id comparison against the oracle, the
+    smallest top-1 minus top-2 logit gap of the oracle's rows."""
+    from tests.greedy_log import RECORDS
+    if not RECORDS:
+        return
+    tr = terminalreporter
+    tr.section("greedy near-tie log (oracle top1 - top2 logit gap)")
+    for what, steps, gap, at, ties in RECORDS:
+        tr.write_line(f"{what}: {steps} greedy steps, min gap {gap:.3e} at step {at}, near ties {ties}")

@@ -12,6 +12,7 @@ import pytest
 
 from rusttorch_amd import synth
 from rusttorch_amd.gpt2 import Gpt2Config, Gpt2Error, Gpt2Model, GenerationConfig
+from tests.greedy_log import assert_ids_equal
 
 pytestmark = pytest.mark.gpu
 
@@ -348,9 +349,9 @@ def test_small_c1_logits_and_ids(O):
     prompt = synth.make_tokens(32, sh.vocab_size)
     om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
     print("[gpu] c1 oracle generate", flush=True)
-    ref_ids = om.generate_cached(prompt, 64)
+    ref_ids, gaps = om.generate_cached(prompt, 64, gaps=True)
     ids = m.generate_cached(prompt, 64, 0.0)
-    assert ids == ref_ids
+    assert_ids_equal(ids, ref_ids, gaps, len(prompt), "c1 small b=1 64 greedy")
     # logits of the prefill and the first 8 decode steps, step by step
     c, oc = m.new_cache(), om.new_cache()
     assert_logits_close(m.forward_cached(prompt, c), om.forward_cached(prompt, oc), "c1 prefill")
@@ -370,7 +371,8 @@ def test_small_batched_matches_single(O):
     # oracle on a slice: 2 sequences, 12 greedy tokens
     om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
     for b in (0, 7):
-        assert om.generate_cached(prompts[b], 12) == out[b, : n + 12].tolist()
+        want, gaps = om.generate_cached(prompts[b], 12, gaps=True)
+        assert_ids_equal(out[b, : n + 12], want, gaps, n, f"c2 small b=8 seq {b} (12 steps)")
 
 
 def _batched_step_logits(O, sd, sh, m, B, n_prompt, n_steps, stream, what):
@@ -415,7 +417,8 @@ def test_batched_step_odd_batch_and_batch_one(O, monkeypatch):
     m1 = Gpt2Model.from_state_dict(sd, cfg_of(sh))
     om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
     prompt = synth.make_tokens(12, sh.vocab_size, stream=520)
-    assert m1.generate_cached(prompt, 16, 0.0) == om.generate_cached(prompt, 16)
+    want, gaps = om.generate_cached(prompt, 16, gaps=True)
+    assert_ids_equal(m1.generate_cached(prompt, 16, 0.0), want, gaps, len(prompt), "small per-op b=1")
     m1.close()
 
 
@@ -459,8 +462,9 @@ def _decode_parity(O, sd, sh, m, n_prompt, n_new, n_logit_steps, stream):
     n_logit_steps single-token steps, against the oracle."""
     om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
     prompt = synth.make_tokens(n_prompt, sh.vocab_size, stream=stream)
-    ref_ids = om.generate_cached(prompt, n_new)
-    assert m.generate_cached(prompt, n_new, 0.0) == ref_ids
+    ref_ids, gaps = om.generate_cached(prompt, n_new, gaps=True)
+    assert_ids_equal(m.generate_cached(prompt, n_new, 0.0), ref_ids, gaps, n_prompt,
+                     f"{sh.n_layer}x{sh.n_embd} b=1 {n_new} greedy")
     c, oc = m.new_cache(), om.new_cache()
     assert_logits_close(m.forward_cached(prompt, c), om.forward_cached(prompt, oc), "prefill")
     for t in range(n_prompt, n_prompt + n_logit_steps):
@@ -531,7 +535,8 @@ def test_xl_bf16_decode(O):
     out = m.generate_cached_batched(prompts, 6)
     om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
     for b in range(2):
-        assert out[b].tolist() == om.generate_cached(prompts[b], 6)
+        want, gaps = om.generate_cached(prompts[b], 6, gaps=True)
+        assert_ids_equal(out[b], want, gaps, 8, f"xl bf16 batched seq {b}")
     # the batched decode step's logits with bf16 tiles (16 sequences: every
     # row of the MFMA tile in use)
     _batched_step_logits(O, sd, sh, m, 16, 4, 1, 480, "xl bf16 b=16")
@@ -560,7 +565,8 @@ def test_batch_above_16_per_op_fallback(O):
     om = O.OracleModel.from_shape(sd, sh)
     for b in (0, 7, 19):
         assert out[b].tolist() == m.generate_cached(prompts[b], 10, 0.0)
-        assert out[b].tolist() == om.generate_cached(prompts[b], 10)
+        want, gaps = om.generate_cached(prompts[b], 10, gaps=True)
+        assert_ids_equal(out[b], want, gaps, 6, f"small b=20 seq {b}")
 
 
 def test_bf16_storage_matches_oracle(O):
@@ -570,7 +576,8 @@ def test_bf16_storage_matches_oracle(O):
     om = O.OracleModel.from_shape(sd, sh)
     ids = synth.make_tokens(24, sh.vocab_size, stream=5)
     assert_logits_close(m.forward(ids), om.forward(ids), "bf16 forward")
-    assert m.generate_cached(ids[:8], 30, 0.0) == om.generate_cached(ids[:8], 30)
+    want, gaps = om.generate_cached(ids[:8], 30, gaps=True)
+    assert_ids_equal(m.generate_cached(ids[:8], 30, 0.0), want, gaps, 8, "mini bf16 b=1")
 
 
 # ---------------------------------------------------------------------------

@@ -147,6 +147,35 @@ def test_argmax_special_cases(O):  # strict '>' from -inf (:858-868)
     assert O.argmax([-np.inf, -np.inf]) == 0
 
 
+def test_top2_gap_brute_force(O):
+    """The near-tie diagnostic: top-1 minus top-2 over the values above
+    -inf with NaN skipped, 0 for a tie at the top, against a sort."""
+    assert O.top2_gap([1.0, 3.0, 3.0]) == 0.0
+    assert O.top2_gap([np.nan, 2.0, 1.5]) == 0.5
+    assert O.top2_gap([1.0]) == np.inf and O.top2_gap([-np.inf, 4.0]) == np.inf
+    rng = np.random.default_rng(11)
+    for _ in range(200):
+        x = rng.standard_normal(int(rng.integers(2, 300))).astype(np.float32)
+        x[rng.random(x.size) < 0.05] = np.nan
+        v = np.sort(x[~np.isnan(x)])
+        if v.size >= 2:
+            assert O.top2_gap(x) == np.float32(v[-1] - v[-2])
+
+
+def test_generate_cached_gaps_follow_the_rows(rand_tiny, O):
+    """generate_cached(gaps=True): same ids as without, and gap s is the
+    top-2 gap of the row greedy step s chose from (teacher forcing)."""
+    _, om = rand_tiny
+    prompt = [1, 5, 9]
+    ids, gaps = om.generate_cached(prompt, 6, gaps=True)
+    assert ids == om.generate_cached(prompt, 6) and gaps.shape == (6,)
+    c = om.new_cache()
+    row = om.forward_cached(prompt, c)[-1]
+    for s in range(6):
+        assert gaps[s] == np.float32(O.top2_gap(row))
+        row = om.forward_cached([ids[3 + s]], c)[0]
+
+
 def test_deterministic_greedy(const_model):  # :1248-1257
     assert const_model.generate([0, 1], 5) == const_model.generate([0, 1], 5)
 
