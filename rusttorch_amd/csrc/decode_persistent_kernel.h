@@ -241,21 +241,11 @@ __device__ __forceinline__ float wsum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
-// Wave-wide sum through DPP (no LDS round trips): butterfly within each
-// 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_ror:4, row_ror:8), then the
-// four row sums are read out with v_readlane. Returns a wave-uniform value.
+// DPP lane move within 16-lane rows (quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] =
+// 0x4E, row_ror:4 = 0x124, row_ror:8 = 0x128): four of them sum a row.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float wsum_dpp(float v) {
-  v += dpp_mov<0xB1>(v);
-  v += dpp_mov<0x4E>(v);
-  v += dpp_mov<0x124>(v);
-  v += dpp_mov<0x128>(v);
-  const int b = __float_as_int(v);
-  return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
-         (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
 }
 // Combine each lane's value with the lane 16 (or 32) apart through gfx950's
 // v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip): the two
@@ -304,9 +294,13 @@ template <>
 struct V16<W_F32> {
   typedef f4v T;
   static constexpr int E = 4;
-  __device__ __forceinline__ static float dot(const T& w, const float* x) {
-    const float4 xv = *reinterpret_cast<const float4*>(x);
-    return w.x * xv.x + w.y * xv.y + w.z * xv.z + w.w * xv.w;
+  // the 16-byte quads of x one weight vector pairs with, and their dot product
+  static constexpr int XQ = 1;
+  __device__ __forceinline__ static void load_x(float4 (&xq)[XQ], const float* x) {
+    xq[0] = *reinterpret_cast<const float4*>(x);
+  }
+  __device__ __forceinline__ static float dot(const T& w, const float4 (&xq)[XQ]) {
+    return w.x * xq[0].x + w.y * xq[0].y + w.z * xq[0].z + w.w * xq[0].w;
   }
 };
 template <>
@@ -314,9 +308,14 @@ struct V16<W_BF16> {
   typedef u4v T;
   static constexpr int E = 8;
   // bf16_to_f32 = bits << 16 (nn/safetensors.rs:389-391)
-  __device__ __forceinline__ static float dot(const T& w, const float* x) {
-    const float4 a = *reinterpret_cast<const float4*>(x);
-    const float4 c = *reinterpret_cast<const float4*>(x + 4);
+  // the 16-byte quads of x one weight vector pairs with, and their dot product
+  static constexpr int XQ = 2;
+  __device__ __forceinline__ static void load_x(float4 (&xq)[XQ], const float* x) {
+    xq[0] = *reinterpret_cast<const float4*>(x);
+    xq[1] = *reinterpret_cast<const float4*>(x + 4);
+  }
+  __device__ __forceinline__ static float dot(const T& w, const float4 (&xq)[XQ]) {
+    const float4 a = xq[0], c = xq[1];
     float s = __uint_as_float(w.x << 16) * a.x + __uint_as_float(w.x & 0xffff0000u) * a.y;
     s += __uint_as_float(w.y << 16) * a.z + __uint_as_float(w.y & 0xffff0000u) * a.w;
     s += __uint_as_float(w.z << 16) * c.x + __uint_as_float(w.z & 0xffff0000u) * c.y;
@@ -380,48 +379,72 @@ __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], co
   }
 }
 
+// Sum over the wave, in every lane: DPP within each 16-lane row, then the
+// permlane swaps across rows (VALU only, no readlane or LDS, so independent
+// sums interleave).
+__device__ __forceinline__ float wave_sum_all(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  return xor32_sum(xor16_sum(v));
+}
+
+// The wave's segments [s0, s0 + SPW) cover pieces of at most NPC rows (whole
+// rows when the geometry is aligned). Every segment's products are summed
+// lane-wise per piece, each piece's lane sums reduced over the wave (the
+// NPC reductions independent of each other), and lane k < SPW then writes
+// slot s0 + k: its piece's sum if segment k ends the piece, else 0, so that a
+// row's slots add up to its dot product.
 template <int WT, int MAXSEG, class GEO>
 __device__ __forceinline__ void seg_compute(const typename V16<WT>::T (&buf)[MAXSEG], const float* x, float* part,
                                             int wg, int cw, int lane, int seg_base) {
-  constexpr int E = V16<WT>::E;
+  constexpr int E = V16<WT>::E, SPR = GEO::SPR, SPW = GEO::SPW;
+  constexpr int NPC = GEO::ALIGNED ? SPW / SPR : (SPW + SPR - 2) / SPR + 1;
   const int row0 = wg * GEO::RPW;
   const int rows_here = min(GEO::RPW, GEO::N - row0);
-  const int segs_here = rows_here > 0 ? rows_here * GEO::SPR : 0;
-  const int s0 = seg_base + cw * GEO::SPW;
-  const int nseg = min(GEO::SPW, segs_here - s0);
-  if constexpr (GEO::ALIGNED) {
-    // The wave owns whole rows: each lane sums its products over a row's SPR
-    // segments and the wave reduces once per row. The row sum goes to the
-    // part slot of the row's last segment, zeros to the others. (Zero-page
-    // segments past nseg are whole rows too and are not stored.)
-    float run = 0.f;
+  const int segs_here = rows_here > 0 ? rows_here * SPR : 0;
+  const int s0 = seg_base + cw * SPW;
+  const int nseg = min(SPW, segs_here - s0);
+  const int j0 = GEO::ALIGNED ? 0 : s0 % SPR;  // aligned: every wave range starts a row
+  // x of every segment first (the LDS reads in flight together) where that
+  // takes at most 64 registers, else segment by segment (wider bf16 shapes
+  // would spill)
+  constexpr int XQ = V16<WT>::XQ;
+  constexpr bool PRE = MAXSEG * XQ * 4 <= 64;
+  float4 xq[PRE ? MAXSEG : 1][XQ];
+  if constexpr (PRE) {
 #pragma unroll
-    for (int i = 0; i < GEO::SPW; ++i) {
-      const int j = i % GEO::SPR;
-      const int v = j * 64 + lane;
-      const float d = V16<WT>::dot(buf[i], x + min(v, GEO::VR - 1) * E);
-      run += v < GEO::VR ? d : 0.f;
-      if (j == GEO::SPR - 1) {
-        const float acc = wsum_dpp(run);
-        run = 0.f;
-        if (lane == 0 && i < nseg) part[s0 + i] = acc;
-      } else if (lane == 0 && i < nseg) {
-        part[s0 + i] = 0.f;
+    for (int i = 0; i < MAXSEG; ++i)
+      if (i < SPW) V16<WT>::load_x(xq[i], x + min(((j0 + i) % SPR) * 64 + lane, GEO::VR - 1) * E);
+  }
+  float r[NPC];
+#pragma unroll
+  for (int q = 0; q < NPC; ++q) r[q] = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXSEG; ++i) {
+    if (i < SPW) {
+      const int v = ((j0 + i) % SPR) * 64 + lane;
+      if constexpr (!PRE) V16<WT>::load_x(xq[0], x + min(v, GEO::VR - 1) * E);
+      const float d = v < GEO::VR ? V16<WT>::dot(buf[i], xq[PRE ? i : 0]) : 0.f;
+      if constexpr (GEO::ALIGNED) {
+        r[i / SPR] += d;
+      } else {
+        const int pc = (j0 + i) / SPR;
+#pragma unroll
+        for (int q = 0; q < NPC; ++q) r[q] += pc == q ? d : 0.f;
       }
     }
-  } else {
-    // Rows span waves: one reduction per segment.
-    int j = s0 % GEO::SPR;
+  }
 #pragma unroll
-    for (int i = 0; i < MAXSEG; ++i) {
-      if (i < GEO::SPW) {
-        const int v = j * 64 + lane;
-        const float d = V16<WT>::dot(buf[i], x + min(v, GEO::VR - 1) * E);
-        const float acc = wsum_dpp(v < GEO::VR ? d : 0.f);
-        if (lane == 0 && i < nseg) part[s0 + i] = acc;
-      }
-      if (++j == GEO::SPR) j = 0;
-    }
+  for (int q = 0; q < NPC; ++q) r[q] = wave_sum_all(r[q]);
+  if (lane < SPW && lane < nseg) {
+    const int pc = (j0 + lane) / SPR;
+    const bool ends = (j0 + lane) % SPR == SPR - 1 || lane == SPW - 1;
+    float val = 0.f;
+#pragma unroll
+    for (int q = 0; q < NPC; ++q) val = pc == q ? r[q] : val;
+    part[s0 + lane] = ends ? val : 0.f;
   }
 }
 
@@ -584,16 +607,6 @@ template <int D>
 __device__ __forceinline__ void glue_input_done(Smem<D>& sm, int ph, int lane) {
   lds_release();
   if (lane == 0) lds_add(&sm.in_ready[ph], 1);
-}
-
-// Sum over the wave, returned to every lane: DPP within each 16-lane row,
-// then the permlane swaps across rows.
-__device__ __forceinline__ float wave_sum_all(float v) {
-  v += dpp_mov<0xB1>(v);
-  v += dpp_mov<0x4E>(v);
-  v += dpp_mov<0x124>(v);
-  v += dpp_mov<0x128>(v);
-  return xor32_sum(xor16_sum(v));
 }
 
 // Leader only: LayerNorm statistics of src[D] (gpt2.rs:636-666, two-pass:
