@@ -1071,6 +1071,152 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny16_kernel(const float* __r
   }
 }
 
+// Prompt GEMM for 17..32 rows with f32 weights, K % 64 == 0: gemm_lds_kernel's
+// LDS-direct ring (4 stages, XOR-swizzled 16-byte chunks, k permuted inside a
+// tile) with a 32 x 128 tile: the 32 rows of A and 128 rows of W (output
+// columns) per 16-k stage, wave w computing columns [32w, 32w + 32) with one
+// v_mfma_f32_32x32x2f32 block. The weights stream as whole 64-byte row runs
+// (four lanes per row), where gemm_skinny_kernel's register loads give each
+// lane its own row (32 lines per wave instruction). Each wave loads two of
+// the eight W groups and one A group (waves 2 and 3 repeat A's into a spare
+// region, so that every wave issues the same three loads per stage).
+// With ks > 1, column block b over k-split z = blockIdx.x / nnb stores its raw
+// tile to ws[z] for splitk_reduce_kernel.
+constexpr int SL_BN = 128;
+constexpr int SL_STAGE = (4 + 8) * 256;  // floats per stage: A groups 0-1 (2-3 spare), W groups 0-7
+template <int ST>
+__device__ __forceinline__ void sl_step(int kt, int nk, float (&stg)[SL_STAGE], float (&nxt)[SL_STAGE],
+                                        const float* asrc, const float* const (&wsrc)[2], int wave,
+                                        const int (&aoff)[2], const int (&woff)[2], floatx16& acc) {
+  // tile kt has landed once at most the loads of the GL_NS - 2 later tiles
+  // (3 instructions each) are outstanding; after the barrier no wave reads
+  // tile kt - 1 any more
+  if (kt + GL_NS - 2 < nk) gl_wait_barrier<(GL_NS - 2) * 3>();
+  else gl_wait_barrier<0>();
+  if (kt + GL_NS - 1 < nk) {
+    const int k = (kt + GL_NS - 1) * 16;
+    gl_dma16(asrc + k, &nxt[wave * 256]);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) gl_dma16(wsrc[q] + k, &nxt[(4 + 2 * wave + q) * 256]);
+  }
+  float4 a[2], b[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    a[c] = *reinterpret_cast<const float4*>(&stg[aoff[c]]);
+    b[c] = *reinterpret_cast<const float4*>(&stg[4 * 256 + woff[c]]);
+  }
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const float4& av = a[st >> 2];
+    const float4& bv = b[st >> 2];
+    const int e = st & 3;
+    const float x = e == 0 ? av.x : e == 1 ? av.y : e == 2 ? av.z : av.w;
+    const float y = e == 0 ? bv.x : e == 1 ? bv.y : e == 2 ? bv.z : bv.w;
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc, 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(256) void gemm_skinny_lds_kernel(const float* __restrict__ A, int lda,
+                                                              const float* __restrict__ W,
+                                                              const float* __restrict__ bias, float* __restrict__ C,
+                                                              long ldc, int M, int N, int K, int epi, int ks,
+                                                              float* __restrict__ ws) {
+  __shared__ __attribute__((aligned(16))) float st0[SL_STAGE];
+  __shared__ __attribute__((aligned(16))) float st1[SL_STAGE];
+  __shared__ __attribute__((aligned(16))) float st2[SL_STAGE];
+  __shared__ __attribute__((aligned(16))) float st3[SL_STAGE];
+  static_assert(GL_NS == 4, "four stage arrays");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nnb = (N + SL_BN - 1) / SL_BN;
+  const int n0 = (blockIdx.x % nnb) * SL_BN, z = blockIdx.x / nnb;
+  const int nk = K / 16 / ks;  // k-tiles of this split, a multiple of GL_NS
+  // load sources: A group wave & 1, W groups 2*wave and 2*wave + 1
+  const int lr = lane >> 2;
+  const float* asrc;
+  const float* wsrc[2];
+  {
+    const int row = (wave & 1) * 16 + lr;
+    const int c = (lane & 3) ^ gl_swz(row);
+    asrc = A + (size_t)min(row, M - 1) * lda + c * 4 + (size_t)z * nk * 16;
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = (2 * wave + q) * 16 + lr;
+    const int c = (lane & 3) ^ gl_swz(row);
+    wsrc[q] = W + (size_t)min(n0 + row, N - 1) * K + c * 4 + (size_t)z * nk * 16;
+  }
+  auto issue = [&](int kt, float (&stg)[SL_STAGE]) {
+    gl_dma16(asrc + kt * 16, &stg[wave * 256]);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) gl_dma16(wsrc[q] + kt * 16, &stg[(4 + 2 * wave + q) * 256]);
+  };
+  // operand reads: A row lane % 32, W row 32*wave + lane % 32, chunks 2h, 2h + 1
+  const int h = lane >> 5;
+  int aoff[2], woff[2];
+  {
+    const int ra = lane & 31, rw = 32 * wave + (lane & 31);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      aoff[c] = ra * 16 + (((2 * h + c) ^ gl_swz(ra)) * 4);
+      woff[c] = rw * 16 + (((2 * h + c) ^ gl_swz(rw)) * 4);
+    }
+  }
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  issue(0, st0);
+  issue(1, st1);
+  issue(2, st2);
+  for (int kt = 0; kt < nk; kt += GL_NS) {
+    sl_step<0>(kt, nk, st0, st3, asrc, wsrc, wave, aoff, woff, acc);
+    sl_step<1>(kt + 1, nk, st1, st0, asrc, wsrc, wave, aoff, woff, acc);
+    sl_step<2>(kt + 2, nk, st2, st1, asrc, wsrc, wave, aoff, woff, acc);
+    sl_step<3>(kt + 3, nk, st3, st2, asrc, wsrc, wave, aoff, woff, acc);
+  }
+  // lane holds C[(e / 4) * 8 + h * 4 + e % 4][n0 + 32 * wave + lane % 32]
+  const int n = n0 + 32 * wave + (lane & 31);
+  if (n >= N) return;
+  if (ws != nullptr) {
+    float* wz = ws + (size_t)z * M * N;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = (e >> 2) * 8 + h * 4 + (e & 3);
+      if (m < M) wz[(size_t)m * N + n] = acc[e];
+    }
+    return;
+  }
+  const float bv = bias ? bias[n] : 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int m = (e >> 2) * 8 + h * 4 + (e & 3);
+    if (m >= M) continue;
+    float* cp = C + (size_t)m * ldc + n;
+    const float v = acc[e];
+    if (epi == EPI_BIAS) *cp = v + bv;
+    else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
+    else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
+    else *cp = v;
+  }
+}
+
+// k-splits of gemm_skinny_lds_kernel: 1 when its column blocks give >= 192
+// workgroups, else the smallest split into whole 4-tile stages giving >= 240,
+// or the largest such split up to 16 (c1's 32-token prefill: 0.72 ms with
+// at most 16, 0.73 with 12, 0.75 with 8, 0.76 with up to 48, whose
+// reductions read 48 partials per output).
+static int skinny_lds_splitk_factor(int M, int N, int K) {
+  const int tiles = (N + SL_BN - 1) / SL_BN;
+  if (M > 32 || M <= 16 || K % 64 != 0 || tiles >= 192) return 1;
+  const int nk = K / 16;
+  int best = 1;
+  for (int sp = 2; sp <= nk / GL_NS && sp <= 16; ++sp) {
+    if ((nk / GL_NS) % sp != 0) continue;
+    best = sp;
+    if (tiles * sp >= 240) break;
+  }
+  return best;
+}
+
 // k-splits of gemm_skinny_kernel (rows M <= 64, 32 x 32 tiles): 1 when the
 // tiles give >= 192 workgroups, else the smallest split of K into multiples
 // of 64 giving >= 240, or the largest valid one up to 16.
@@ -1094,6 +1240,18 @@ static bool launch_skinny(hipStream_t s, const float* A, int lda, const void* W,
                           float* C, long ldc, int M, int N, int K, int epi, const SkinnyQkv& qkv, float* ws,
                           size_t ws_floats, KvDst kv_pre, int kv_T, int kv_past) {
   if (M > 64 || K % 64 != 0 || lda % 4 != 0) return false;
+  if (wtype == W_F32 && M > 16 && M <= 32 && qkv.q == nullptr && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(W) & 15) == 0) {
+    int ks = skinny_lds_splitk_factor(M, N, K);
+    if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
+    if (ks > 1 || kv_pre.k == nullptr) {
+      const int nnb = (N + SL_BN - 1) / SL_BN;
+      gemm_skinny_lds_kernel<<<nnb * ks, 256, 0, s>>>(A, lda, static_cast<const float*>(W), bias, C, ldc, M, N, K,
+                                                      epi, ks, ks > 1 ? ws : nullptr);
+      if (ks > 1) splitk_reduce(s, ws, ks, M, N, bias, C, ldc, epi, kv_pre, kv_T, kv_past);
+      return true;
+    }
+  }
   int ks = qkv.q == nullptr ? skinny_splitk_factor(M, N, K) : 1;
   if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
   if (ks > 1) {
@@ -1135,8 +1293,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= (long)M * N) return;
   const int m = (int)(i / N), n = (int)(i - (long)m * N);
+  // the partials in flight eight at a time, summed in z order
   float v = ws[i];
-  for (int z = 1; z < ks; ++z) v += ws[(size_t)z * M * N + i];
+  int z = 1;
+  for (; z + 8 <= ks; z += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = ws[(size_t)(z + u) * M * N + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += t[u];
+  }
+  for (; z < ks; ++z) v += ws[(size_t)z * M * N + i];
   const float bv = bias ? bias[n] : 0.f;
   if (kv.k != nullptr && n >= kv.d) {
     const int which = n >= 2 * kv.d, cc = n - kv.d - which * kv.d;
@@ -1183,7 +1350,7 @@ size_t gemm_splitk_ws_floats(int M, int N, int K) {
   // the larger of the two kernels' needs (which one runs depends on the
   // weight type and alignment)
   const int ks = std::max(std::max(gemm_splitk_factor(M, N, K, GL_NS), gemm_splitk_factor(M, N, K, 1)),
-                          skinny_splitk_factor(M, N, K));
+                          std::max(skinny_splitk_factor(M, N, K), skinny_lds_splitk_factor(M, N, K)));
   return ks > 1 ? (size_t)ks * M * N : 0;
 }
 
