@@ -440,6 +440,25 @@ def test_long_prefill_attention_blocks(O):
         assert_logits_close(lg2[b], om.forward_cached(ids[b, n1:], oc), f"second chunk seq {b}")
 
 
+def test_short_prompt_gemms_17_to_32_rows(O):
+    """Prompts of 17-32 rows run their GEMMs on gemm_skinny_lds_kernel (a
+    32 x 128 tile over an LDS ring, rows past the prompt clamped, k split
+    into whole 4-tile stages): every row's logits against the oracle for
+    17, 24, 31 and 32 new tokens, the last two appended to a cache that
+    already holds 9 tokens (the c_attn split's reduction writes K/V at
+    past + t), and a prompt of 16 rows beside them (gemm_skinny16_kernel)."""
+    sd, sh, m = gpu_model("small")
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    for n, past in ((16, 0), (17, 0), (24, 0), (31, 9), (32, 9)):
+        ids = synth.make_tokens(past + n, sh.vocab_size, stream=800 + n)
+        c, oc = m.new_cache(), om.new_cache()
+        if past:
+            m.forward_cached(ids[:past], c)
+            om.forward_cached(ids[:past], oc)
+        assert_logits_close(m.forward_cached(ids[past:], c), om.forward_cached(ids[past:], oc),
+                            f"{n} new rows after {past}")
+
+
 def test_batched_forward_logits(O):
     sd, sh, m = gpu_model("mini")
     B, n = 3, 10
