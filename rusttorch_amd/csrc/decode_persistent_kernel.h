@@ -125,11 +125,12 @@ constexpr int TRACE_N = 1536;
   } while (0)
 
 // Row split of one GEMV phase: N outputs, each a dot product over K inputs
-// stored as VR 16-byte vectors; a segment = 64 vectors of one row.
-template <int N_, int K_, int E_, int SPW_ = 0>
+// stored as VR 16-byte vectors; a segment = 64 vectors of one row. The rows
+// go to the first GW_ workgroups (RPW each); the others own none.
+template <int N_, int K_, int E_, int SPW_ = 0, int GW_ = G>
 struct Geom {
   static constexpr int N = N_, K = K_, VR = K_ / E_, SPR = (VR + 63) / 64;
-  static constexpr int RPW = (N_ + G - 1) / G;
+  static constexpr int RPW = (N_ + GW_ - 1) / GW_;  // rows of each of the first GW_ workgroups
   static constexpr int SW = slot_words(RPW);  // exchange slot of one workgroup's rows
   static constexpr int SEGS = RPW * SPR;
   // Segments per GEMV wave: an even split, rounded up to whole rows unless
@@ -154,7 +155,11 @@ struct Cfg {
   // tokens/s non-temporal), non-temporal otherwise (c3: 1.54k against 1.53k)
   static constexpr bool LM_NT = D_ != 768;
   typedef Geom<3 * D, D, E> GQ;
-  typedef Geom<D, D, E> GP;
+  // the attention projection on the first D / 8 workgroups, 8 rows each: its
+  // input then goes to (and x2 comes from) 96 workgroups at d = 768 instead
+  // of 256 (c1: 209.5 against 215.5 µs per token; 4 rows: 215.5, 6: 211.6,
+  // 12: 210.0, 16: 212.1; c3: 591 against 596.5)
+  typedef Geom<D, D, E, 0, (D + 7) / 8> GP;
   typedef Geom<4 * D, D, E> GF;
   typedef Geom<D, 4 * D, E> GM;
   static constexpr int MAXSEG = cmax(cmax(GQ::SPW, GP::SPW), cmax(GF::SPW, GM::SPW));
@@ -985,7 +990,9 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const float bias = leader && lane < rows_here ? PK_G(float, LP.baproj)[row0 + lane] : 0.f;
       // the heads' normalised outputs are the projection input: published by
       // the attention items themselves (one chunk per head) or by the mergers
-      glue_fetch<HD, ITEM_SLOT, H * HD>(T + (NCH == 1 ? p.o_att : p.o_head), H * HD, tag, sm.in_vec[0], gl, p.err);
+      if (rows_here > 0)  // workgroups without projection rows count themselves in without the input
+        glue_fetch<HD, ITEM_SLOT, H * HD>(T + (NCH == 1 ? p.o_att : p.o_head), H * HD, tag, sm.in_vec[0], gl,
+                                          p.err);
       glue_input_done(sm, PH_PROJ, lane);
       if (leader) {
         PK_TRACE(p, tb + 5, lane);
