@@ -147,10 +147,11 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 template <int D_, int V_, int WT_>
 struct Cfg {
   static constexpr int D = D_, V = V_, WT = WT_, H = D_ / HD, E = WT_ == W_BF16 ? 8 : 4;
-  // refill pacing (seg_issue): measured best at 8 for d = 768 (c1: 4.29k
-  // against 4.21k tokens/s at 12) and at 12 for d = 1024 (c3: 1.54k against
-  // 1.51k at 8); 12 elsewhere
-  static constexpr int PACE = D_ == 768 ? 8 : PK_PACE;
+  // refill pacing (seg_issue): measured best at 8 for d = 768 (c1: 210.3 µs
+  // per token against 209.9 at 6, 211.5 at 4, 218.8 at 12) and at 6 for
+  // d = 1024 (c3: 582.5 µs against 582.8 at 4, 593 at 8, 590.5 at 12, 594
+  // at 2); 12 elsewhere
+  static constexpr int PACE = D_ == 768 ? 8 : D_ == 1024 ? 6 : PK_PACE;
   // the tied LM head's loads: normal for d = 768 (c1: 4.38k against 4.29k
   // tokens/s non-temporal), non-temporal otherwise (c3: 1.54k against 1.53k)
   static constexpr bool LM_NT = D_ != 768;
