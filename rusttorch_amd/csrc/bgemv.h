@@ -28,11 +28,12 @@ struct BgemvArgs {
   long ldc;
   int epi;
   BgemvQkv qkv;
-  // LayerNorm folded in (ln_g set): x is scaled by ln_g[k] as it is read and
-  // the epilogue computes inv_std * (acc - mean * ln_s[n]) before the bias
-  // (then the folded constant c[n]). The statistics of input row m come from
-  // the partials the kernel that wrote x left in ln_part[g][m] = (mean, M2)
-  // over columns [g * ln_cols, (g + 1) * ln_cols) of K, g < ln_groups <= 128.
+  // LayerNorm folded in (ln_g set): X holds x already scaled by the gain
+  // ln_g[k] (written so by the kernel that produced x, see xg below), and the
+  // epilogue computes inv_std * (acc - mean * ln_s[n]) before the bias (then
+  // the folded constant c[n]). The statistics of input row m come from the
+  // partials the kernel that wrote x left in ln_part[g][m] = (mean, M2) over
+  // columns [g * ln_cols, (g + 1) * ln_cols) of K, g < ln_groups <= 128.
   const float* ln_g;
   const float* ln_s;
   const float* ln_part;
@@ -40,8 +41,11 @@ struct BgemvArgs {
   float eps;
   // Residual epilogue only: writes those partials for the rows it wrote,
   // stats_part[g][m] for its panel groups g (plan.groups * 32 floats), with
-  // groups of 16 * plan.npw columns.
+  // groups of 16 * plan.npw columns; with xg set, also xg[m][n] = y * g_next[n]
+  // (row stride ldc), the input of the next LayerNorm-folded GEMV.
   float* stats_part;
+  float* xg;
+  const float* g_next;
   // LM head: per-row packed argmax keys (gpt2.rs:858-868), updated with a
   // device-scope atomic max (zero before; the step's finalize resets them).
   unsigned long long* keys;
@@ -68,10 +72,12 @@ BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force = 0, int s_force = 0
 bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a);
 size_t bgemv_work_floats(const BgemvPlan& pl);
 bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a);
-// Decode embedding x[r] = wte[token[r]] + wpe[*pos_dev] of rows r < rows and
+// Decode embedding x[r] = wte[token[r]] + wpe[*pos_dev] of rows r < rows,
+// xg[r] = x[r] * g (the input of the LayerNorm-folded GEMV that follows) and
 // their LayerNorm statistics partials as one group of width d: part[r] =
 // (mean, M2) (the ln_part of the following GEMV, ln_groups = 1). d <= 2048.
 bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
-                        const int* pos_dev, int rows, int d, float* x, float* part);
+                        const int* pos_dev, int rows, int d, float* x, float* part, const float* g,
+                        float* xg);
 
 }  // namespace rtg

@@ -63,9 +63,10 @@ __global__ __launch_bounds__(64 * BG_NW) void bgemv_kernel(BgemvArgs a) {
 }
 
 // k-tiles a wave keeps in flight: its whole chunk at once when that fits
-// the register budget (about 160 registers of tiles), else a ring of 4.
-int bgemv_depth(const BgemvPlan& pl, int wtype, bool lng) {
-  const int per_tile = 4 * pl.npw + (wtype == W_F32 ? 4 : 8) * (lng ? 2 : 1);
+// the register budget (about 160 registers of tiles: weights and x), else a
+// ring of 4.
+int bgemv_depth(const BgemvPlan& pl, int wtype) {
+  const int per_tile = 4 * pl.npw + (wtype == W_F32 ? 4 : 8);
   for (int d : {8, 12})
     if (pl.ktc <= d && per_tile * d <= 160) return d;
   return 4;
@@ -79,7 +80,8 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
                                                           const float* __restrict__ wpe,
                                                           const uint32_t* __restrict__ token,
                                                           const int* __restrict__ pos_dev, int d,
-                                                          float* __restrict__ x, float* __restrict__ part) {
+                                                          float* __restrict__ x, float* __restrict__ part,
+                                                          const float* __restrict__ g, float* __restrict__ xg) {
   __shared__ float red[4];
   const int b = blockIdx.x, tid = threadIdx.x;
   const long tok = token[b];
@@ -95,6 +97,7 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
                                      : __uint_as_float((uint32_t)static_cast<const uint16_t*>(wte)[tok * d + k] << 16);
       v[i] = w + wpe[(long)pos * d + k];
       x[(long)b * d + k] = v[i];
+      xg[(long)b * d + k] = v[i] * g[k];
       s += v[i];
     }
   }
@@ -137,14 +140,14 @@ bool launch_tile_weights(hipStream_t s, const void* src, int wtype, int N, int K
 
 BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force, int s_force, int nw) {
   // Measured on MI355X over the GPT-2 decode shapes (2304..50257 rows, K 768..6400,
-  // f32 and bf16): two panels per wave once there are >= 300 panels (four for
-  // the bf16 LM head), one below; the k range split over 5 workgroups for K >= 150 tiles (a wave's
+  // f32 and bf16): two panels per wave once there are >= 300 panels (for the
+  // LM head four with bf16 weights, one with f32: 29.6 against 33.3 µs with two), one below; the k range split over 5 workgroups for K >= 150 tiles (a wave's
   // chunk then fits in flight at once: c5 2.69 -> 2.58 ms per step against 4; 2 and 8 were slower on
   // c2), over 2 for fewer than 120 panels (too few workgroups otherwise), else not at all.
   BgemvPlan pl{};
   const int TK = wtype == W_F32 ? 16 : 32;
   const int KT = K / TK, NP = (N + 15) / 16;
-  pl.npw = npw_force > 0 ? npw_force : (NP >= 1500 && wtype == W_BF16 ? 4 : NP >= 300 ? 2 : 1);
+  pl.npw = npw_force > 0 ? npw_force : (NP >= 1500 ? (wtype == W_BF16 ? 4 : 1) : NP >= 300 ? 2 : 1);
   int S = s_force > 0 ? s_force : (KT >= 150 ? 5 : (NP < 120 ? 2 : 1));
   if (S < 1) S = 1;
   if (S > bgc::SMAX) S = bgc::SMAX;
@@ -178,7 +181,7 @@ bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
   a.ktc = pl.ktc;
   const dim3 grid(pl.groups, pl.S);
   const dim3 block(64 * BG_NW);
-  const int depth = bgemv_depth(pl, a.wtype, a.ln_g != nullptr);
+  const int depth = bgemv_depth(pl, a.wtype);
 #define BG_LAUNCH_D(WT, NPW, LNG)                                                         \
   do {                                                                                    \
     if (depth == 12) bgemv_kernel<WT, NPW, LNG, 12, true><<<grid, block, 0, s>>>(a);      \
@@ -205,9 +208,10 @@ bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
 }
 
 bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
-                        const int* pos_dev, int rows, int d, float* x, float* part) {
+                        const int* pos_dev, int rows, int d, float* x, float* part, const float* g,
+                        float* xg) {
   if (d > 2048) return false;
-  embed_stats_kernel<<<rows, 256, 0, s>>>(wte, wtype, wpe, token, pos_dev, d, x, part);
+  embed_stats_kernel<<<rows, 256, 0, s>>>(wte, wtype, wpe, token, pos_dev, d, x, part, g, xg);
   return hipGetLastError() == hipSuccess;
 }
 

@@ -192,7 +192,6 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
   }
   const int xr = min(r, a.M - 1);
   const float* xrow = a.X + (size_t)xr * a.ldx + t0 * TK + q * E;
-  const float* grow = a.ln_g + t0 * TK + q * E;  // LayerNorm gain at the same k (LNG)
   floatx4 acc[NPW];
 #pragma unroll
   for (int j = 0; j < NPW; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -201,16 +200,12 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
   // consumed) so that the load sequence stays branch-free
   Raw w[DEPTH_][NPW];
   f4v x[DEPTH_][E / 4];
-  f4v gv[LNG ? DEPTH_ : 1][E / 4];
   auto issue = [&](int slot, int i) {
     const int ti = min(i, max(nt - 1, 0));
 #pragma unroll
     for (int j = 0; j < NPW; ++j) w[slot][j] = __builtin_nontemporal_load(wp[j] + (size_t)ti * 64);
 #pragma unroll
-    for (int h = 0; h < E / 4; ++h) {
-      x[slot][h] = *reinterpret_cast<const f4v*>(xrow + ti * TK + 4 * h);
-      if constexpr (LNG) gv[slot][h] = *reinterpret_cast<const f4v*>(grow + ti * TK + 4 * h);
-    }
+    for (int h = 0; h < E / 4; ++h) x[slot][h] = *reinterpret_cast<const f4v*>(xrow + ti * TK + 4 * h);
   };
   // one tile: acc += x . w over its TK inputs
   auto consume = [&](int d) {
@@ -222,10 +217,7 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
       // measured ~10% faster, with half the error against a float64 sum)
       float xs[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xs[e] = x[d][e >> 2][e & 3];
-        if constexpr (LNG) xs[e] *= gv[d][e >> 2][e & 3];
-      }
+      for (int e = 0; e < 8; ++e) xs[e] = x[d][e >> 2][e & 3];
       u4v xh, xm, xl;
       split3(xs, xh, xm, xl);
 #pragma unroll
@@ -238,8 +230,7 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        float xa = x[d][e >> 2][e & 3];
-        if constexpr (LNG) xa *= gv[d][e >> 2][e & 3];
+        const float xa = x[d][e >> 2][e & 3];
 #pragma unroll
         for (int j = 0; j < NPW; ++j)
           acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, TL::get(w[d][j], e), acc[j], 0, 0, 0);
@@ -355,6 +346,7 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
       float t = v[j];
       if constexpr (LNG) t = inv_std * (t - mean * a.ln_s[n]);
       y[j] = store_out(a, m, n, t);
+      if (a.xg) a.xg[(size_t)m * a.ldc + n] = y[j] * a.g_next[n];
       if (a.keys) {
         const u64 k = argmax_key(y[j], (uint32_t)n);
         best = k > best ? k : best;

@@ -421,15 +421,21 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
   auto run = [&](const BgemvPlan& pl, const BgemvArgs& a) {
     if (!launch_bgemv(s, pl, a)) throw HipError{"bgemv launch failed"};
   };
-  if (!launch_embed_stats(s, m->wte, m->wtype, m->wpe, c->token_dev, c->pos_dev, B, d, c->x, c->bg_spart))
+  // c->ln holds x scaled by the gain of the LayerNorm folded into the next
+  // GEMV (written by the embedding and by each residual epilogue)
+  const size_t NL = m->layers.size();
+  if (!launch_embed_stats(s, m->wte, m->wtype, m->wpe, c->token_dev, c->pos_dev, B, d, c->x, c->bg_spart,
+                          NL ? m->layers[0].ln1w : m->lnfw, c->ln))
     throw HipError{"embed_stats launch failed"};
   // shape of the statistics partials the last residual writer left
   int st_groups = 1, st_cols = d;
   auto ln_in = [&](BgemvArgs& a, const float* g, const float* sv) {
     a.ln_g = g; a.ln_s = sv; a.ln_part = c->bg_spart; a.ln_groups = st_groups; a.ln_cols = st_cols;
   };
-  auto resid_out = [&](BgemvArgs& a, const BgemvPlan& pl) {
+  auto resid_out = [&](BgemvArgs& a, const BgemvPlan& pl, const float* g_next) {
     a.stats_part = c->bg_spart;
+    a.xg = c->ln;
+    a.g_next = g_next;
     st_groups = pl.groups;
     st_cols = 16 * pl.npw;
   };
@@ -439,7 +445,7 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
     KvDst kv = kv_layer(c, l);
     {  // LN1 + c_attn; k/v of the new token into the cache
       BgemvArgs a = base();
-      a.X = c->x; a.ldx = d; a.Wt = T.qkv; a.N = 3 * d; a.K = d; a.bias = T.cq;
+      a.X = c->ln; a.ldx = d; a.Wt = T.qkv; a.N = 3 * d; a.K = d; a.bias = T.cq;
       ln_in(a, L.ln1w, T.sq);
       a.epi = EPI_BIAS;
       a.qkv = BgemvQkv{c->qkv, d, d, kv, c->pos_dev};
@@ -450,12 +456,12 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
       BgemvArgs a = base();
       a.X = c->att; a.ldx = d; a.Wt = T.proj; a.N = d; a.K = d; a.bias = L.baproj;
       a.C = c->x; a.ldc = d; a.epi = EPI_BIAS_RESID;
-      resid_out(a, bw->pp);
+      resid_out(a, bw->pp, L.ln2w);
       run(bw->pp, a);
     }
     {  // LN2 + c_fc + gelu_new
       BgemvArgs a = base();
-      a.X = c->x; a.ldx = d; a.Wt = T.fc; a.N = 4 * d; a.K = d; a.bias = T.cf;
+      a.X = c->ln; a.ldx = d; a.Wt = T.fc; a.N = 4 * d; a.K = d; a.bias = T.cf;
       ln_in(a, L.ln2w, T.sf);
       a.C = c->h; a.ldc = 4 * d; a.epi = EPI_BIAS_GELU;
       run(bw->pf, a);
@@ -464,13 +470,13 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
       BgemvArgs a = base();
       a.X = c->h; a.ldx = 4 * d; a.Wt = T.mproj; a.N = d; a.K = 4 * d; a.bias = L.bmproj;
       a.C = c->x; a.ldc = d; a.epi = EPI_BIAS_RESID;
-      resid_out(a, bw->pm);
+      resid_out(a, bw->pm, l + 1 < NL ? m->layers[l + 1].ln1w : m->lnfw);
       run(bw->pm, a);
     }
   }
   {  // ln_f + tied LM head (gpt2.rs:392-396)
     BgemvArgs a = base();
-    a.X = c->x; a.ldx = d; a.Wt = bw->lm; a.N = V; a.K = d; a.bias = bw->cl;
+    a.X = c->ln; a.ldx = d; a.Wt = bw->lm; a.N = V; a.K = d; a.bias = bw->cl;
     ln_in(a, m->lnfw, bw->sl);
     a.C = c->logits; a.ldc = V; a.epi = EPI_BIAS;
     run(bw->pl, a);
