@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kernels.h"
+
 namespace rtg {
 
 constexpr int AD_ITEM = 2 + 64;  // per-wave softmax state: m, l, o[64]
@@ -97,12 +99,14 @@ __device__ __forceinline__ void af_window(const float4 (&k4)[AF_RG], const float
 // cache, each window's K/V rows loaded while the previous one is computed
 // (two register sets), with an online softmax per wave (16 lanes per row, 4
 // dims each, DPP row sums). The wave states (m, l, o) merge in LDS (wp,
-// [NWV][AD_ITEM]) in wave order; out[b][h*64 + d] = o / l. Every thread of the
+// [NWV][AD_ITEM]) in wave order; out[b][h*64 + d] = o / l (row stride ldo),
+// or with out_tk > 0 at xt_index(b, h*64 + d, B, out_tk). Every thread of the
 // workgroup calls it.
 template <int NWV>
 __device__ __forceinline__ void attn_item(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
                                           const float* __restrict__ vc, int H, int P, int len, int h, int b,
-                                          float* __restrict__ out, int ldo, float (*wp)[AD_ITEM]) {
+                                          float* __restrict__ out, int ldo, int out_tk, int B,
+                                          float (*wp)[AD_ITEM]) {
   constexpr int WR = 4 * AF_RG;  // rows per window
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, grp = lane >> 4, dq = (lane & 15) * 4;
   const size_t head_off = ((size_t)b * H + h) * (size_t)P * 64;
@@ -154,7 +158,8 @@ __device__ __forceinline__ void attn_item(const float* __restrict__ q, int ldq, 
       Ls += wp[w][1] * f;
       o += wp[w][2 + tid] * f;
     }
-    out[(size_t)b * ldo + h * 64 + tid] = o / Ls;
+    const size_t oi = out_tk ? xt_index(b, h * 64 + tid, B, out_tk) : (size_t)b * ldo + h * 64 + tid;
+    out[oi] = o / Ls;
   }
   __syncthreads();  // wp is free again
 }

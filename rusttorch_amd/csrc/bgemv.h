@@ -19,14 +19,21 @@ struct BgemvQkv {
 };
 
 struct BgemvArgs {
-  const float* X;  // [M][ldx] f32 inputs, M <= 16
-  int ldx, M;
+  // f32 inputs of M <= 16 rows in the GEMV input layout: element (m, k) at
+  // xt_index(m, k, M, TK) (kernels.h), TK = 16 for f32 weights, 32 for bf16
+  const float* X;
+  int M;
   const void* Wt;  // tile-ordered weights (launch_tile_weights)
   int wtype, N, K;
   const float* bias;  // [N] or null
   float* C;           // [M][ldc] output (plain epilogues)
   long ldc;
   int epi;
+  // C written in the input layout of the next GEMV instead (xt_index with
+  // this GEMV's M and TK; ldc unused): the gelu_new epilogue of c_fc, whose
+  // output only the MLP projection reads. Not with the residual or QKV
+  // epilogues.
+  bool c_tiled;
   BgemvQkv qkv;
   // LayerNorm folded in (ln_g set): X holds x already scaled by the gain
   // ln_g[k] (written so by the kernel that produced x, see xg below), and the
@@ -41,8 +48,9 @@ struct BgemvArgs {
   float eps;
   // Residual epilogue only: writes those partials for the rows it wrote,
   // stats_part[g][m] for its panel groups g (plan.groups * 32 floats), with
-  // groups of 16 * plan.npw columns; with xg set, also xg[m][n] = y * g_next[n]
-  // (row stride ldc), the input of the next LayerNorm-folded GEMV.
+  // groups of 16 * plan.npw columns; with xg set, also y * g_next[n] to xg in
+  // the input layout (xt_index(m, n, M, TK)), the input of the next
+  // LayerNorm-folded GEMV.
   float* stats_part;
   float* xg;
   const float* g_next;
@@ -73,9 +81,10 @@ bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a);
 size_t bgemv_work_floats(const BgemvPlan& pl);
 bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a);
 // Decode embedding x[r] = wte[token[r]] + wpe[*pos_dev] of rows r < rows,
-// xg[r] = x[r] * g (the input of the LayerNorm-folded GEMV that follows) and
-// their LayerNorm statistics partials as one group of width d: part[r] =
-// (mean, M2) (the ln_part of the following GEMV, ln_groups = 1). d <= 2048.
+// x[r] * g in the GEMV input layout to xg (xt_index(r, k, rows, TK of wtype):
+// the input of the LayerNorm-folded GEMV that follows) and their LayerNorm
+// statistics partials as one group of width d: part[r] = (mean, M2) (the
+// ln_part of the following GEMV, ln_groups = 1). d <= 2048.
 bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
                         const int* pos_dev, int rows, int d, float* x, float* part, const float* g,
                         float* xg);

@@ -72,8 +72,9 @@ int bgemv_depth(const BgemvPlan& pl, int wtype) {
   return 4;
 }
 
-// Decode embedding of B rows (gpt2.rs:377-384: wte[token] + wpe[position])
-// and the rows' LayerNorm statistics partials as one group of width d
+// Decode embedding of B rows (gpt2.rs:377-384: wte[token] + wpe[position]),
+// x * g in the GEMV input layout, and the rows' LayerNorm statistics
+// partials as one group of width d
 // (part[m] = (mean, M2), two passes as layer_norm, gpt2.rs:636-666): one
 // workgroup of 256 threads per row.
 __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict__ wte, int wtype,
@@ -84,6 +85,7 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
                                                           const float* __restrict__ g, float* __restrict__ xg) {
   __shared__ float red[4];
   const int b = blockIdx.x, tid = threadIdx.x;
+  const int tk = wtype == W_F32 ? 16 : 32;  // xg in the GEMV input layout
   const long tok = token[b];
   const int pos = *pos_dev;
   float v[8];  // d <= 2048
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
                                      : __uint_as_float((uint32_t)static_cast<const uint16_t*>(wte)[tok * d + k] << 16);
       v[i] = w + wpe[(long)pos * d + k];
       x[(long)b * d + k] = v[i];
-      xg[(long)b * d + k] = v[i] * g[k];
+      xg[xt_index(b, k, gridDim.x, tk)] = v[i] * g[k];
       s += v[i];
     }
   }
@@ -164,7 +166,8 @@ BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force, int s_force, int nw
 
 bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a) {
   const int TK = a.wtype == W_F32 ? 16 : 32;
-  if (a.M < 1 || a.M > 16 || a.K % TK != 0 || a.ldx % 4 != 0) return false;
+  if (a.M < 1 || a.M > 16 || a.K % TK != 0) return false;
+  if (a.c_tiled && (a.epi == EPI_BIAS_RESID || a.qkv.q || a.N % TK != 0)) return false;
   if (pl.S < 1 || pl.S > bgc::SMAX || (pl.S > 1 && (!a.part || !a.cnt))) return false;
   if (a.ln_g && (!a.ln_s || !a.ln_part || a.ln_groups < 1 || a.ln_groups > 16 * bgc::LNG_PER || a.ln_cols < 1 ||
                  (a.ln_groups - 1) * a.ln_cols >= a.K || a.ln_groups * a.ln_cols < a.K))
@@ -210,7 +213,7 @@ bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
 bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
                         const int* pos_dev, int rows, int d, float* x, float* part, const float* g,
                         float* xg) {
-  if (d > 2048) return false;
+  if (d > 2048 || d % (wtype == W_F32 ? 16 : 32) != 0) return false;
   embed_stats_kernel<<<rows, 256, 0, s>>>(wte, wtype, wpe, token, pos_dev, d, x, part, g, xg);
   return hipGetLastError() == hipSuccess;
 }

@@ -31,6 +31,19 @@ struct KvDst {
   int d;           // n_embd
 };
 
+// Input layout of the batched decode GEMV (bgemv.hip): element (m, k) of an
+// M-row input read in k-tiles of tk columns (16 for f32 weights, 32 for bf16)
+// sits at [k / tk][chunk][m][k % 4], with the 4-column chunks c = (k % tk) / 4
+// of a tile in the order the GEMV's lanes load them (for tk = 32, lane group
+// g of 16 lanes holds columns 8g..8g+7 and loads them as two 16-byte halves,
+// so the half-h chunks of all groups come first). One 16-byte load of a lane
+// group then reads M rows of one chunk contiguously. M = 1 is row order.
+__host__ __device__ inline size_t xt_index(int m, int k, int M, int tk) {
+  const int c = (k % tk) >> 2;
+  const int pos = tk == 32 ? ((c & 1) << 2) | (c >> 1) : c;
+  return ((size_t)(k / tk) * (tk >> 2) + pos) * (size_t)M * 4 + (size_t)m * 4 + (k & 3);
+}
+
 // Token + position embedding. ids[rows]; position of row r = pos0 + (r % T),
 // or, when pos_dev != nullptr, *pos_dev (decode: T == 1).
 void launch_embed(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* ids, int rows, int T,
@@ -49,9 +62,10 @@ void launch_gemv_qkv(hipStream_t s, int B, const void* W, int wtype, const float
                      float* q, int ldq, int d, KvDst kv, const int* pos_dev);
 
 // Decode attention over the cache for positions [0, *pos_dev] (gpt2.rs:772-834),
-// one new token per sequence.
+// one new token per sequence. out[b][ldo] rows, or with out_tk > 0 (head_dim
+// 64 only) the GEMV input layout xt_index(b, col, B, out_tk).
 void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc,
-                        int n_head, int n_pos, const int* pos_dev, float* out, int ldo);
+                        int n_head, int n_pos, const int* pos_dev, float* out, int ldo, int out_tk = 0);
 
 // Greedy argmax over rows of logits (gpt2.rs:858-868) into packed keys.
 void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V, unsigned long long* keys);

@@ -376,7 +376,7 @@ void launch_gemv_qkv(hipStream_t s, int B, const void* W, int wtype, const float
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, int ldq,
                                                           const float* __restrict__ kc, const float* __restrict__ vc,
                                                           int H, int P, int hd, const int* __restrict__ pos_dev,
-                                                          float* __restrict__ out, int ldo) {
+                                                          float* __restrict__ out, int ldo, int out_tk) {
   extern __shared__ float sm[];
   float* qs = sm;          // [hd]
   float* red = sm + 64;    // [16] block reduction scratch
@@ -414,7 +414,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     for (int j = part; j < len; j += 4) acc = fmaf(sc[j], Vh[(size_t)j * hd + dd], acc);
   pv[part * 64 + dd] = acc;
   __syncthreads();
-  if (tid < hd) out[(size_t)b * ldo + h * hd + tid] = (pv[tid] + pv[64 + tid]) + (pv[128 + tid] + pv[192 + tid]);
+  if (tid < hd) {
+    const size_t oi = out_tk ? xt_index(b, h * hd + tid, gridDim.y, out_tk) : (size_t)b * ldo + h * hd + tid;
+    out[oi] = (pv[tid] + pv[64 + tid]) + (pv[128 + tid] + pv[192 + tid]);
+  }
 }
 
 // Decode attention for head_dim 64 in one kernel: block (h, b) of NWV waves
@@ -424,25 +427,29 @@ __global__ __launch_bounds__(64 * NWV) void attn_decode_fused_kernel(const float
                                                                     const float* __restrict__ kc,
                                                                     const float* __restrict__ vc, int H, int P,
                                                                     const int* __restrict__ pos_dev,
-                                                                    float* __restrict__ out, int ldo) {
+                                                                    float* __restrict__ out, int ldo, int out_tk) {
   __shared__ float wp[NWV][AD_ITEM];
-  attn_item<NWV>(q, ldq, kc, vc, H, P, *pos_dev + 1, blockIdx.x, blockIdx.y, out, ldo, wp);
+  attn_item<NWV>(q, ldq, kc, vc, H, P, *pos_dev + 1, blockIdx.x, blockIdx.y, out, ldo, out_tk, gridDim.y, wp);
 }
 
 void launch_attn_decode(hipStream_t s, int B, const float* q, int ldq, const float* kc, const float* vc, int n_head,
-                        int n_pos, const int* pos_dev, float* out, int ldo) {
+                        int n_pos, const int* pos_dev, float* out, int ldo, int out_tk) {
   // head_dim = ldq-independent: derived by the caller into n_head via ldo.
   const int hd = ldo / n_head;
   if (hd == 64) {
     // 16 waves per (head, sequence) while there are fewer pairs than CUs
     if (n_head * B < 256)
-      attn_decode_fused_kernel<16><<<dim3(n_head, B), 1024, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, out, ldo);
+      attn_decode_fused_kernel<16>
+          <<<dim3(n_head, B), 1024, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, out, ldo, out_tk);
     else
-      attn_decode_fused_kernel<8><<<dim3(n_head, B), 512, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, out, ldo);
+      attn_decode_fused_kernel<8>
+          <<<dim3(n_head, B), 512, 0, s>>>(q, ldq, kc, vc, n_head, n_pos, pos_dev, out, ldo, out_tk);
     return;
   }
+
   const size_t smem = (336 + (size_t)n_pos) * sizeof(float);
-  attn_decode_kernel<<<dim3(n_head, B), 256, smem, s>>>(q, ldq, kc, vc, n_head, n_pos, hd, pos_dev, out, ldo);
+  attn_decode_kernel<<<dim3(n_head, B), 256, smem, s>>>(q, ldq, kc, vc, n_head, n_pos, hd, pos_dev, out, ldo,
+                                                        out_tk);
 }
 
 // ---------------------------------------------------------------------------

@@ -422,7 +422,9 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
     if (!launch_bgemv(s, pl, a)) throw HipError{"bgemv launch failed"};
   };
   // c->ln holds x scaled by the gain of the LayerNorm folded into the next
-  // GEMV (written by the embedding and by each residual epilogue)
+  // GEMV (written by the embedding and by each residual epilogue); c->ln,
+  // c->att and c->h are in the GEMV input layout (xt_index, tile width tk)
+  const int tk = m->wtype == W_F32 ? 16 : 32;
   const size_t NL = m->layers.size();
   if (!launch_embed_stats(s, m->wte, m->wtype, m->wpe, c->token_dev, c->pos_dev, B, d, c->x, c->bg_spart,
                           NL ? m->layers[0].ln1w : m->lnfw, c->ln))
@@ -445,30 +447,30 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
     KvDst kv = kv_layer(c, l);
     {  // LN1 + c_attn; k/v of the new token into the cache
       BgemvArgs a = base();
-      a.X = c->ln; a.ldx = d; a.Wt = T.qkv; a.N = 3 * d; a.K = d; a.bias = T.cq;
+      a.X = c->ln; a.Wt = T.qkv; a.N = 3 * d; a.K = d; a.bias = T.cq;
       ln_in(a, L.ln1w, T.sq);
       a.epi = EPI_BIAS;
       a.qkv = BgemvQkv{c->qkv, d, d, kv, c->pos_dev};
       run(bw->pq, a);
     }
-    launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d);
+    launch_attn_decode(s, B, c->qkv, d, kv.k, kv.v, kv.n_head, kv.n_pos, c->pos_dev, c->att, d, tk);
     {  // attention c_proj + residual; statistics partials for LN2
       BgemvArgs a = base();
-      a.X = c->att; a.ldx = d; a.Wt = T.proj; a.N = d; a.K = d; a.bias = L.baproj;
+      a.X = c->att; a.Wt = T.proj; a.N = d; a.K = d; a.bias = L.baproj;
       a.C = c->x; a.ldc = d; a.epi = EPI_BIAS_RESID;
       resid_out(a, bw->pp, L.ln2w);
       run(bw->pp, a);
     }
     {  // LN2 + c_fc + gelu_new
       BgemvArgs a = base();
-      a.X = c->ln; a.ldx = d; a.Wt = T.fc; a.N = 4 * d; a.K = d; a.bias = T.cf;
+      a.X = c->ln; a.Wt = T.fc; a.N = 4 * d; a.K = d; a.bias = T.cf;
       ln_in(a, L.ln2w, T.sf);
-      a.C = c->h; a.ldc = 4 * d; a.epi = EPI_BIAS_GELU;
+      a.C = c->h; a.c_tiled = true; a.epi = EPI_BIAS_GELU;
       run(bw->pf, a);
     }
     {  // mlp c_proj + residual; statistics partials for the next LayerNorm
       BgemvArgs a = base();
-      a.X = c->h; a.ldx = 4 * d; a.Wt = T.mproj; a.N = d; a.K = 4 * d; a.bias = L.bmproj;
+      a.X = c->h; a.Wt = T.mproj; a.N = d; a.K = 4 * d; a.bias = L.bmproj;
       a.C = c->x; a.ldc = d; a.epi = EPI_BIAS_RESID;
       resid_out(a, bw->pm, l + 1 < NL ? m->layers[l + 1].ln1w : m->lnfw);
       run(bw->pm, a);
@@ -476,7 +478,7 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
   }
   {  // ln_f + tied LM head (gpt2.rs:392-396)
     BgemvArgs a = base();
-    a.X = c->ln; a.ldx = d; a.Wt = bw->lm; a.N = V; a.K = d; a.bias = bw->cl;
+    a.X = c->ln; a.Wt = bw->lm; a.N = V; a.K = d; a.bias = bw->cl;
     ln_in(a, m->lnfw, bw->sl);
     a.C = c->logits; a.ldc = V; a.epi = EPI_BIAS;
     run(bw->pl, a);
