@@ -142,15 +142,19 @@ bool launch_tile_weights(hipStream_t s, const void* src, int wtype, int N, int K
 
 BgemvPlan bgemv_plan(int N, int K, int wtype, int npw_force, int s_force, int nw) {
   // Measured on MI355X over the GPT-2 decode shapes (2304..50257 rows, K 768..6400,
-  // f32 and bf16): two panels per wave once there are >= 300 panels (for the
-  // LM head four with bf16 weights, one with f32: 29.6 against 33.3 µs with two), one below; the k range split over 5 workgroups for K >= 150 tiles (a wave's
-  // chunk then fits in flight at once: c5 2.69 -> 2.58 ms per step against 4; 2 and 8 were slower on
-  // c2), over 2 for fewer than 120 panels (too few workgroups otherwise), else not at all.
+  // f32 and bf16, whole decode steps): two panels per wave once there are >= 300
+  // panels (for the LM head four with bf16 weights, one with f32: 29.6 against
+  // 33.3 µs with two), one below; K >= 150 tiles (the MLP projection) splits
+  // the k range over 5 workgroups with two panels per wave for bf16 (c5 2138 ->
+  // 2104 µs per step against one panel; 4 splits 2215) and over 4 for f32 (c2
+  // 380 -> 377 µs against 5); shorter k ranges are not split (the attention
+  // projection: c2 390 -> 380 µs against 2 splits).
   BgemvPlan pl{};
   const int TK = wtype == W_F32 ? 16 : 32;
   const int KT = K / TK, NP = (N + 15) / 16;
-  pl.npw = npw_force > 0 ? npw_force : (NP >= 1500 ? (wtype == W_BF16 ? 4 : 1) : NP >= 300 ? 2 : 1);
-  int S = s_force > 0 ? s_force : (KT >= 150 ? 5 : (NP < 120 ? 2 : 1));
+  const bool bf = wtype == W_BF16;
+  pl.npw = npw_force > 0 ? npw_force : (NP >= 1500 ? (bf ? 4 : 1) : NP >= 300 || (bf && KT >= 150) ? 2 : 1);
+  int S = s_force > 0 ? s_force : (KT >= 150 ? (bf ? 5 : 4) : 1);
   if (S < 1) S = 1;
   if (S > bgc::SMAX) S = bgc::SMAX;
   pl.ktc = (KT + S * nw - 1) / (S * nw);
