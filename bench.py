@@ -110,6 +110,11 @@ def cpu_baseline(sd, sh, prompt, n_decode, all_threads, what):
 
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
+# dense bf16 MFMA peak; a GEMM with bf16 weights runs each f32 product as
+# three exact bf16 MFMA products (the activation split into three bf16
+# parts), so its peak in f32 flops is a third of it
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+BF16X3_PEAK_TFLOPS = MFMA_BF16_PEAK_TFLOPS / 3
 PREFILL_WORKLOADS = {
     # name: (shape, batch, tokens): forward_cached on an empty cache, full [T, V] logits per sequence
     "c4": ("large", 32, 1024),
@@ -203,17 +208,23 @@ def prefill_bytes(sh, B, T, wbytes):
 
 def prefill_roofline(sh, B, T, wbytes, ms):
     """Roofline of the prefill leg: HBM when its arithmetic intensity is
-    below the fp32 ridge (157.3 TFLOP/s / 8 TB/s), MFMA fp32 otherwise."""
+    below the MFMA ridge (peak / 8 TB/s), MFMA otherwise. The peak is fp32
+    MFMA for f32 weights; for bf16 weights the GEMMs run on bf16 MFMA with
+    three exact products per f32 product (mfma "bf16x3"), so the peak in
+    algorithmic f32 flops is the dense bf16 peak / 3."""
     flops = prefill_flops(sh, B, T)
     nbytes = prefill_bytes(sh, B, T, wbytes)
     s = ms / 1e3
-    if flops / nbytes < MFMA_FP32_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+    bf16 = wbytes == 2
+    peak = BF16X3_PEAK_TFLOPS if bf16 else MFMA_FP32_PEAK_TFLOPS
+    if flops / nbytes < peak * 1e12 / (HBM_PEAK_GBS * 1e9):
         ach = nbytes / s / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "bytes": int(nbytes), "ms": round(ms, 4)}
     ach = flops / s / 1e12
-    return {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(ach / MFMA_FP32_PEAK_TFLOPS, 4), "flops": int(flops), "ms": round(ms, 4)}
+    return {"bound": "mfma", "mfma": "bf16x3" if bf16 else "fp32", "achieved": round(ach, 2),
+            "peak": round(peak, 1), "unit": "TFLOP/s", "frac": round(ach / peak, 4), "flops": int(flops),
+            "ms": round(ms, 4)}
 
 
 def calib_copy(nbytes):

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "argmax_key.h"
+#include "bf16_split.h"
 
 #include "bgemv.h"
 
@@ -20,31 +21,7 @@ typedef unsigned long long u64;
 constexpr int DEPTH = 4;    // k-tiles in flight per wave of the streaming (ring) form
 constexpr int SMAX = 8;     // most workgroups per panel group
 constexpr int LNG_PER = 8;  // statistics groups per lane (ln_groups <= 128)
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// x as the exact sum hi + mid + lo of three bf16 values (each the top 16
-// bits of an f32: hi = x truncated to bf16, mid = (x - hi) truncated, lo =
-// x - hi - mid, whose at most 8 significant bits fit bf16 exactly), packed
-// for the A operand of v_mfma_f32_16x16x32_bf16: dword i of a level holds
-// elements 2i (low half) and 2i + 1.
-__device__ __forceinline__ void split3(const float (&x)[8], u4v& hi, u4v& mid, u4v& lo) {
-  unsigned bh[8], bm[8], bl[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const unsigned xb = __float_as_uint(x[e]);
-    bh[e] = xb & 0xffff0000u;
-    const float r1 = x[e] - __uint_as_float(bh[e]);
-    bm[e] = __float_as_uint(r1) & 0xffff0000u;
-    bl[e] = __float_as_uint(r1 - __uint_as_float(bm[e]));
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    hi[i] = __builtin_amdgcn_perm(bh[2 * i + 1], bh[2 * i], 0x07060302u);
-    mid[i] = __builtin_amdgcn_perm(bm[2 * i + 1], bm[2 * i], 0x07060302u);
-    lo[i] = __builtin_amdgcn_perm(bl[2 * i + 1], bl[2 * i], 0x07060302u);
-  }
-}
-__device__ __forceinline__ bf16x8 as_bf16x8(const u4v& v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ float gelu_new_b(float x) {
   const float sqrt_2_pi = 0.7978845608028654f;  // gpt2.rs:837-847, the reference's association

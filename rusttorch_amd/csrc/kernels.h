@@ -91,8 +91,9 @@ void launch_kv_append(hipStream_t s, const float* qkv, int S, int T, int past, K
 // Prefill c_attn: C = A W^T + bias with the k/v columns ([d, 3d)) of row
 // s*T + t written into the cache at position past + t instead of C (the
 // append of LayerKVCache::append, gpt2.rs:500-514, in the GEMM's epilogue).
-// Falls back to launch_gemm + launch_kv_append where the fused kernel does not
-// apply (f32 weights, K % 64 == 0, 16-byte aligned operands, more than 64 rows).
+// Falls back to launch_gemm + launch_kv_append where the fused kernels do not
+// apply (they need K % 64 == 0, 16-byte aligned operands and more than 64
+// rows; f32 or bf16 weights).
 void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
                      long ldc, int M, int K, int S, int T, int past, KvDst kv, float* ws = nullptr,
                      size_t ws_floats = 0);

@@ -12,6 +12,7 @@
 
 #include "argmax_key.h"
 #include "attn_core.h"
+#include "bf16_split.h"
 #include "kernels.h"
 
 namespace rtg {
@@ -760,6 +761,67 @@ __device__ __forceinline__ void gl_step(int kt, int nk, float (&lds)[2][GBM * 16
   }
 }
 
+// Epilogue of the 128x128 tile kernels: wave tile (wm, wn) of block (m0, n0)
+// in acc[i][j] (32x32 blocks, MFMA output layout), to ws[z] as a raw partial
+// tile when ws is set, else with the epilogue (bias, gelu, residual; with kv
+// set, c_attn's k / v columns go into the cache at (sequence, head, past + t)).
+__device__ __forceinline__ void gl_epilogue(const floatx16 (&acc)[2][2], int lane, int m0, int n0, int wm, int wn,
+                                            int z, const float* __restrict__ bias, float* __restrict__ C, long ldc,
+                                            int M, int N, int epi, const KvDst& kv, int kv_T, int kv_past,
+                                            float* __restrict__ ws) {
+  if (ws != nullptr) {
+    float* wz = ws + (size_t)z * M * N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn + j * 32 + (lane & 31);
+        if (n >= N) continue;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (m < M) wz[(size_t)m * N + n] = acc[i][j][e];
+        }
+      }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn + j * 32 + (lane & 31);
+      if (n >= N) continue;
+      const float bv = bias ? bias[n] : 0.f;
+      if (kv.k != nullptr && n >= kv.d) {
+        // k / v column of c_attn: into the cache at (sequence, head, past + t)
+        const int which = n >= 2 * kv.d, cc = n - kv.d - which * kv.d;
+        float* base = (which ? kv.v : kv.k) + (size_t)(cc >> 6) * kv.n_pos * 64 + (cc & 63);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (m < M) {
+            const int sq = m / kv_T, t = m - sq * kv_T;
+            base[((size_t)sq * kv.n_head * kv.n_pos + kv_past + t) * 64] = acc[i][j][e] + bv;
+          }
+        }
+        continue;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (m < M) {
+          float* cp = C + (size_t)m * ldc + n;
+          const float v = acc[i][j][e];
+          if (epi == EPI_BIAS) *cp = v + bv;
+          else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
+          else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
+          else *cp = v;
+        }
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__ A, int lda,
                                                        const float* __restrict__ W, const float* __restrict__ bias,
                                                        float* __restrict__ C, long ldc, int M, int N, int K, int epi,
@@ -835,57 +897,123 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__
     gl_step<3>(kt + 3, nk, st3, st2, asrc, wsrc, wave, aoff, woff, acc);
   }
 
-  if (ws != nullptr) {
-    float* wz = ws + (size_t)z * M * N;
+  gl_epilogue(acc, lane, m0, n0, wm, wn, z, bias, C, ldc, M, N, epi, kv, kv_T, kv_past, ws);
+}
+
+// gemm_lds_kernel for bf16 weights (the f32 activations times W stored as
+// bf16, gpt2.rs Conv1D with bf16-rounded weights upcast in the product): the
+// same 128x128 tiles, k-tiles of 16 and LDS-direct stage ring, with W's tile
+// as 128 rows of 32 bytes (one load instruction per wave: lane i fills row
+// 32 * wave + i / 2, 16-byte chunk (i % 2) ^ ((row >> 3) & 1)). Each lane's 8
+// A values of a 32-row block enter v_mfma_f32_32x32x16_bf16 as three exact
+// bf16 parts (split3), so every product is exact in f32 and the MFMA
+// accumulates in f32: the f32 GEMM up to summation order, at the bf16 rate.
+// Lane l holds A[row l % 32][k 8 (l / 32) .. + 8) and W[col l % 32][the same
+// k] of a tile, the A reads of gemm_lds_kernel.
+template <int ST>
+__device__ __forceinline__ void glb_step(int kt, int nk, float (&la)[GBM * 16], float (&lw)[GBM * 8],
+                                         float (&na)[GBM * 16], float (&nw)[GBM * 8], const float* const (&asrc)[2],
+                                         const uint16_t* wsrc, int wave, const int (&aoff)[2][2], const int (&woff)[2],
+                                         floatx16 (&acc)[2][2]) {
+  // tile kt has landed once at most the loads of the GL_NS - 2 later tiles
+  // (3 instructions each) are outstanding
+  if (kt + GL_NS - 2 < nk) gl_wait_barrier<(GL_NS - 2) * 3>();
+  else gl_wait_barrier<0>();
+  if (kt + GL_NS - 1 < nk) {
+    const int k = (kt + GL_NS - 1) * 16;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn + j * 32 + (lane & 31);
-        if (n >= N) continue;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-          if (m < M) wz[(size_t)m * N + n] = acc[i][j][e];
-        }
-      }
-    return;
+    for (int q = 0; q < 2; ++q) gl_dma16(asrc[q] + k, &na[(2 * wave + q) * 256]);
+    gl_dma16(reinterpret_cast<const float*>(wsrc + k), &nw[wave * 256]);
   }
+  u4v b[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const u4v*>(&lw[woff[j]]);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
+    const float4 a0 = *reinterpret_cast<const float4*>(&la[aoff[i][0]]);
+    const float4 a1 = *reinterpret_cast<const float4*>(&la[aoff[i][1]]);
+    const float xs[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    u4v xh, xm, xl;
+    split3(xs, xh, xm, xl);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn + j * 32 + (lane & 31);
-      if (n >= N) continue;
-      const float bv = bias ? bias[n] : 0.f;
-      if (kv.k != nullptr && n >= kv.d) {
-        // k / v column of c_attn: into the cache at (sequence, head, past + t)
-        const int which = n >= 2 * kv.d, cc = n - kv.d - which * kv.d;
-        float* base = (which ? kv.v : kv.k) + (size_t)(cc >> 6) * kv.n_pos * 64 + (cc & 63);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-          if (m < M) {
-            const int sq = m / kv_T, t = m - sq * kv_T;
-            base[((size_t)sq * kv.n_head * kv.n_pos + kv_past + t) * 64] = acc[i][j][e] + bv;
-          }
-        }
-        continue;
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (m < M) {
-          float* cp = C + (size_t)m * ldc + n;
-          const float v = acc[i][j][e];
-          if (epi == EPI_BIAS) *cp = v + bv;
-          else if (epi == EPI_BIAS_GELU) *cp = gelu_new(v + bv);
-          else if (epi == EPI_BIAS_RESID) *cp = *cp + (v + bv);
-          else *cp = v;
-        }
-      }
+      const bf16x8 wb = as_bf16x8(b[j]);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xh), wb, acc[i][j], 0, 0, 0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xm), wb, acc[i][j], 0, 0, 0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xl), wb, acc[i][j], 0, 0, 0);
     }
   }
+}
+
+__device__ __forceinline__ int glb_swz(int row) { return (row >> 3) & 1; }
+
+__global__ __launch_bounds__(256) void gemm_lds_bf16_kernel(const float* __restrict__ A, int lda,
+                                                            const uint16_t* __restrict__ W,
+                                                            const float* __restrict__ bias, float* __restrict__ C,
+                                                            long ldc, int M, int N, int K, int epi, int m_fast,
+                                                            KvDst kv, int kv_T, int kv_past, int ks,
+                                                            float* __restrict__ ws) {
+  __shared__ __attribute__((aligned(16))) float a0[GBM * 16], a1[GBM * 16], a2[GBM * 16], a3[GBM * 16];
+  __shared__ __attribute__((aligned(16))) float w0[GBM * 8], w1[GBM * 8], w2[GBM * 8], w3[GBM * 8];
+  static_assert(GL_NS == 4, "four stage arrays");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int nmb = (M + GBM - 1) / GBM, nnb = (N + GBN - 1) / GBN;
+  const int bid = blockIdx.x % (nmb * nnb), z = blockIdx.x / (nmb * nnb);
+  const int m0 = (m_fast ? bid % nmb : bid / nnb) * GBM, n0 = (m_fast ? bid / nmb : bid % nnb) * GBN;
+  const int nk = K / 16 / ks;  // k-tiles of this split, a multiple of GL_NS
+
+  // load sources: A groups 2*wave and 2*wave + 1 (as gemm_lds_kernel), W rows
+  // 32*wave + lane / 2
+  const int lr = lane >> 2;
+  const float* asrc[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = (2 * wave + q) * 16 + lr;
+    const int c = (lane & 3) ^ gl_swz(row);
+    asrc[q] = A + (size_t)min(m0 + row, M - 1) * lda + c * 4 + (size_t)z * nk * 16;
+  }
+  const uint16_t* wsrc;
+  {
+    const int row = 32 * wave + (lane >> 1);
+    const int c = (lane & 1) ^ glb_swz(row);
+    wsrc = W + (size_t)min(n0 + row, N - 1) * K + c * 8 + (size_t)z * nk * 16;
+  }
+  auto issue = [&](int kt, float (&la)[GBM * 16], float (&lw)[GBM * 8]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) gl_dma16(asrc[q] + kt * 16, &la[(2 * wave + q) * 256]);
+    gl_dma16(reinterpret_cast<const float*>(wsrc + kt * 16), &lw[wave * 256]);
+  };
+  // operand reads: A rows wm + 32i + lane % 32, chunks 2h and 2h + 1 (floats);
+  // W rows wn + 32j + lane % 32, chunk h (8 bf16 = 4 floats' bytes)
+  const int h = lane >> 5;
+  int aoff[2][2], woff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ra = wm + 32 * i + (lane & 31), rw = wn + 32 * i + (lane & 31);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) aoff[i][c] = ra * 16 + (((2 * h + c) ^ gl_swz(ra)) * 4);
+    woff[i] = rw * 8 + ((h ^ glb_swz(rw)) * 4);
+  }
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  issue(0, a0, w0);
+  issue(1, a1, w1);
+  issue(2, a2, w2);
+  for (int kt = 0; kt < nk; kt += GL_NS) {
+    glb_step<0>(kt, nk, a0, w0, a3, w3, asrc, wsrc, wave, aoff, woff, acc);
+    glb_step<1>(kt + 1, nk, a1, w1, a0, w0, asrc, wsrc, wave, aoff, woff, acc);
+    glb_step<2>(kt + 2, nk, a2, w2, a1, w1, asrc, wsrc, wave, aoff, woff, acc);
+    glb_step<3>(kt + 3, nk, a3, w3, a2, w2, asrc, wsrc, wave, aoff, woff, acc);
+  }
+  gl_epilogue(acc, lane, m0, n0, wm, wn, z, bias, C, ldc, M, N, epi, kv, kv_T, kv_past, ws);
 }
 
 // Skinny GEMM for few rows (a short prompt): the 128x128 tile kernel would
@@ -1362,26 +1490,27 @@ size_t gemm_splitk_ws_floats(int M, int N, int K) {
 }
 
 static bool gemm_lds_ok(const float* A, int lda, const void* W, int wtype, int K) {
-  return wtype == W_F32 && K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+  return K % 64 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(W) & 15) == 0;
 }
 
-// gemm_lds_kernel, split over k when that fills the GPU and ws holds the
-// partial tiles (ws_floats of them), then the split-k reduction.
-static void launch_gemm_lds(hipStream_t s, const float* A, int lda, const float* W, const float* bias, float* C,
-                            long ldc, int M, int N, int K, int epi, KvDst kv, int kv_T, int kv_past, float* ws,
-                            size_t ws_floats) {
+// gemm_lds_kernel (f32 W) or gemm_lds_bf16_kernel (bf16 W), split over k
+// when that fills the GPU and ws holds the partial tiles (ws_floats of them),
+// then the split-k reduction.
+static void launch_gemm_lds(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias,
+                            float* C, long ldc, int M, int N, int K, int epi, KvDst kv, int kv_T, int kv_past,
+                            float* ws, size_t ws_floats) {
   const int nb = ((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM);
   int ks = gemm_splitk_factor(M, N, K, GL_NS);
   if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
-  if (ks == 1) {
-    gemm_lds_kernel<<<nb, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, N > M ? 1 : 0, kv, kv_T, kv_past, 1,
-                                       nullptr);
-    return;
-  }
-  gemm_lds_kernel<<<nb * ks, 256, 0, s>>>(A, lda, W, bias, C, ldc, M, N, K, epi, N > M ? 1 : 0, kv, kv_T, kv_past,
-                                          ks, ws);
-  splitk_reduce(s, ws, ks, M, N, bias, C, ldc, epi, kv, kv_T, kv_past);
+  float* wsk = ks > 1 ? ws : nullptr;
+  if (wtype == W_F32)
+    gemm_lds_kernel<<<nb * ks, 256, 0, s>>>(A, lda, static_cast<const float*>(W), bias, C, ldc, M, N, K, epi,
+                                            N > M ? 1 : 0, kv, kv_T, kv_past, ks, wsk);
+  else
+    gemm_lds_bf16_kernel<<<nb * ks, 256, 0, s>>>(A, lda, static_cast<const uint16_t*>(W), bias, C, ldc, M, N, K,
+                                                 epi, N > M ? 1 : 0, kv, kv_T, kv_past, ks, wsk);
+  if (ks > 1) splitk_reduce(s, ws, ks, M, N, bias, C, ldc, epi, kv, kv_T, kv_past);
 }
 
 void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtype, const float* bias, float* C,
@@ -1393,8 +1522,7 @@ void launch_gemm(hipStream_t s, const float* A, int lda, const void* W, int wtyp
     // faster on the c4 shapes without an epilogue but made the c4 prefill
     // slower, 70.7k against 72.5k tokens/s; 3 stages at three waves per SIMD
     // and 2 stages at four were no faster than this kernel)
-    launch_gemm_lds(s, A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, epi, KvDst{}, 1, 0, ws,
-                    ws_floats);
+    launch_gemm_lds(s, A, lda, W, wtype, bias, C, ldc, M, N, K, epi, KvDst{}, 1, 0, ws, ws_floats);
   else {
     int ks = gemm_splitk_factor(M, N, K, 1);
     if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
@@ -1410,8 +1538,7 @@ void launch_gemm_qkv(hipStream_t s, const float* A, int lda, const void* W, int 
                      long ldc, int M, int K, int S, int T, int past, KvDst kv, float* ws, size_t ws_floats) {
   const int N = 3 * kv.d;
   if (M > 64 && gemm_lds_ok(A, lda, W, wtype, K) && kv.d == 64 * kv.n_head) {
-    launch_gemm_lds(s, A, lda, reinterpret_cast<const float*>(W), bias, C, ldc, M, N, K, EPI_BIAS, kv, T, past, ws,
-                    ws_floats);
+    launch_gemm_lds(s, A, lda, W, wtype, bias, C, ldc, M, N, K, EPI_BIAS, kv, T, past, ws, ws_floats);
     return;
   }
   // a prompt of at most 64 rows: the split skinny GEMM's reduction writes the
