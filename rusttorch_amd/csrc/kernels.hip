@@ -1652,8 +1652,8 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float* __restric
 
 // ---------------------------------------------------------------------------
 // Prefill causal attention for head_dim 64 on fp32 MFMA (flash-attention
-// form of multi_head_attention_cached, gpt2.rs:772-834). A workgroup of 4
-// waves takes 128 queries of one (sequence, head); each wave owns 32. Key
+// form of multi_head_attention_cached, gpt2.rs:772-834). A workgroup of FW
+// waves takes 32 * FW queries of one (sequence, head); each wave owns 32. Key
 // blocks of 32 rows are staged in LDS (K row-major, V transposed), the next
 // block's rows are loaded into registers while the current one is used.
 //
@@ -1670,14 +1670,15 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float* __restric
 // ---------------------------------------------------------------------------
 
 constexpr int FA_QW = 32;         // queries per wave
-constexpr int FA_W = 4;           // waves per workgroup
 constexpr int FA_K = 32;          // keys per block
 constexpr int FA_KP = 64 + 4;     // padded K row (floats)
 constexpr int FA_VP = FA_K + 4;   // padded V^T row (floats)
 
-__global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
+template <int FW>
+__global__ __launch_bounds__(64 * FW) void attn_prefill_mfma_kernel(
     const float* __restrict__ qkv, int T, int past, const float* __restrict__ kc, const float* __restrict__ vc,
     int H, int P, int d, int nqb, float* __restrict__ out) {
+  constexpr int NT = 64 * FW, U = 512 / NT;  // threads; float4 of K (and of V) a thread stages per block
   __shared__ __attribute__((aligned(16))) float Ks[FA_K][FA_KP];
   __shared__ __attribute__((aligned(16))) float Vt[64][FA_VP];
   // the query block is the slowest grid dimension, longest (last) blocks
@@ -1687,7 +1688,7 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
   const int h = blockIdx.x, sidx = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane & 31, hh = lane >> 5;
-  const int qi = qb * FA_QW * FA_W + wave * FA_QW + c;  // this lane's query (0..T-1 when valid)
+  const int qi = qb * FA_QW * FW + wave * FA_QW + c;  // this lane's query (0..T-1 when valid)
   const bool qvalid = qi < T;
   const int qpos = past + qi;
   const size_t head_off = ((size_t)sidx * H + h) * (size_t)P * 64;
@@ -1706,14 +1707,14 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
       q[4 * j + 3] = v.w;
     }
   }
-  const int kmax = past + min(T, (qb + 1) * FA_QW * FA_W) - 1;  // last key any query here attends
+  const int kmax = past + min(T, (qb + 1) * FA_QW * FW) - 1;  // last key any query here attends
   const int nkb = kmax / FA_K + 1;
-  // staging: 512 float4 of K and of V per block, 2 each per thread
-  float4 kr[2], vr[2];
+  // staging: 512 float4 of K and of V per block, U each per thread
+  float4 kr[U], vr[U];
   auto load_block = [&](int kb) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int e = tid + u * FA_QW * 2 * FA_W;
+    for (int u = 0; u < U; ++u) {
+      const int e = tid + u * NT;
       const int r = e >> 4, c4 = (e & 15) * 4, j = kb * FA_K + r;
       const bool ok = j <= kmax;
       kr[u] = ok ? *reinterpret_cast<const float4*>(Kh + (size_t)j * 64 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1731,8 +1732,8 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
   for (int kb = 0; kb < nkb; ++kb) {
     __syncthreads();  // every wave is done with the previous block
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int e = tid + u * FA_QW * 2 * FA_W;
+    for (int u = 0; u < U; ++u) {
+      const int e = tid + u * NT;
       const int r = e >> 4, c4 = (e & 15) * 4;
       *reinterpret_cast<float4*>(&Ks[r][c4]) = kr[u];
       Vt[c4][r] = vr[u].x;
@@ -1807,12 +1808,202 @@ __global__ __launch_bounds__(FA_QW * 2 * FA_W) void attn_prefill_mfma_kernel(
   }
 }
 
+// attn_prefill_mfma_kernel with the key range split over the waves: a
+// workgroup of KS waves takes 32 queries of one (sequence, head) and wave w
+// the key blocks w, w + KS, ... (each staged in the wave's own LDS region, so
+// no workgroup barrier per block); the waves' (m, l, O) merge in LDS at the
+// end (out = sum_w O_w e^(m_w - M) / sum_w l_w e^(m_w - M)). For a few long
+// prompts the causal chain of the last query block (T / 32 key blocks, one
+// after the other on one wave) is otherwise the whole kernel.
+template <int KS>
+__global__ __launch_bounds__(64 * KS) void attn_prefill_ks_kernel(const float* __restrict__ qkv, int T, int past,
+                                                                  const float* __restrict__ kc,
+                                                                  const float* __restrict__ vc, int H, int P, int d,
+                                                                  int nqb, float* __restrict__ out) {
+  constexpr int REG = FA_K * FA_KP + 64 * FA_VP;  // floats of one wave's K block and V^T block
+  constexpr int MW = 64 + 2;                      // merge record of one query: m, l, O[64]
+  static_assert(FA_QW * MW <= REG, "merge records fit the staging region");
+  __shared__ __attribute__((aligned(16))) float sm[KS][REG];
+  const int qb = nqb - 1 - (int)blockIdx.z;  // longest query blocks first
+  const int h = blockIdx.x, sidx = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = lane & 31, hh = lane >> 5;
+  const int qi = qb * FA_QW + c;
+  const bool qvalid = qi < T;
+  const int qpos = past + qi;
+  const size_t head_off = ((size_t)sidx * H + h) * (size_t)P * 64;
+  const float* Kh = kc + head_off;
+  const float* Vh = vc + head_off;
+  float(*Ks)[FA_KP] = reinterpret_cast<float(*)[FA_KP]>(&sm[wave][0]);
+  float(*Vt)[FA_VP] = reinterpret_cast<float(*)[FA_VP]>(&sm[wave][FA_K * FA_KP]);
+  float q[32];
+  {
+    const float* qrow = qkv + ((size_t)sidx * T + min(qi, T - 1)) * 3 * d + h * 64 + 32 * hh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 v = reinterpret_cast<const float4*>(qrow)[j];
+      q[4 * j] = v.x;
+      q[4 * j + 1] = v.y;
+      q[4 * j + 2] = v.z;
+      q[4 * j + 3] = v.w;
+    }
+  }
+  const int kmax = past + min(T, (qb + 1) * FA_QW) - 1;
+  const int nkb = kmax / FA_K + 1;
+  float4 kr[8], vr[8];
+  auto load_block = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = lane + u * 64;
+      const int r = e >> 4, c4 = (e & 15) * 4, j = kb * FA_K + r;
+      const bool ok = j <= kmax;
+      kr[u] = ok ? *reinterpret_cast<const float4*>(Kh + (size_t)j * 64 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[u] = ok ? *reinterpret_cast<const float4*>(Vh + (size_t)j * 64 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  float m = -INFINITY, l = 0.f;
+  floatx16 o0, o1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    o0[i] = 0.f;
+    o1[i] = 0.f;
+  }
+  if (wave < nkb) load_block(wave);
+  for (int kb = wave; kb < nkb; kb += KS) {
+    // this wave's region only: LDS accesses of one wave are ordered, the
+    // wave's previous reads are complete before its writes below
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = lane + u * 64;
+      const int r = e >> 4, c4 = (e & 15) * 4;
+      *reinterpret_cast<float4*>(&Ks[r][c4]) = kr[u];
+      Vt[c4][r] = vr[u].x;
+      Vt[c4 + 1][r] = vr[u].y;
+      Vt[c4 + 2][r] = vr[u].z;
+      Vt[c4 + 3][r] = vr[u].w;
+    }
+    if (kb + KS < nkb) load_block(kb + KS);
+    floatx16 sc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 a = *reinterpret_cast<const float4*>(&Ks[c][32 * hh + 4 * j]);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, q[4 * j], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, q[4 * j + 1], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, q[4 * j + 2], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, q[4 * j + 3], sc, 0, 0, 0);
+    }
+    const int j0 = kb * FA_K;
+    float bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int j = j0 + (i / 4) * 8 + hh * 4 + (i % 4);
+      sc[i] = j <= qpos ? sc[i] * 0.125f : -INFINITY;
+      bm = fmaxf(bm, sc[i]);
+    }
+    bm = xor32_max_k(bm);
+    const float mn = fmaxf(m, bm);
+    const float corr = m == -INFINITY ? 0.f : fexp_a(m - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      sc[i] = sc[i] == -INFINITY ? 0.f : fexp_a(sc[i] - mn);
+      ps += sc[i];
+    }
+    l = l * corr + ps;
+    m = mn;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      o0[i] *= corr;
+      o1[i] *= corr;
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 v0 = *reinterpret_cast<const float4*>(&Vt[c][8 * g + 4 * hh]);
+      const float4 v1 = *reinterpret_cast<const float4*>(&Vt[32 + c][8 * g + 4 * hh]);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.x, sc[4 * g], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.x, sc[4 * g], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.y, sc[4 * g + 1], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.y, sc[4 * g + 1], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.z, sc[4 * g + 2], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.z, sc[4 * g + 2], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0.w, sc[4 * g + 3], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1.w, sc[4 * g + 3], o1, 0, 0, 0);
+    }
+  }
+  l = xor32_sum_k(l);
+  // merge records: query c of wave w at sm[w][c * MW]: m, l, O[64]
+  __syncthreads();  // every wave is done with its staging region
+  float* rec = &sm[wave][c * MW];
+  if (hh == 0) {
+    rec[0] = m;
+    rec[1] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = (i / 4) * 8 + hh * 4 + (i % 4);
+    rec[2 + r] = o0[i];
+    rec[2 + 32 + r] = o1[i];
+  }
+  __syncthreads();
+  // wave 0 lane (c, hh) merges the 32 dims it holds for query c
+  if (wave == 0 && qvalid) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < KS; ++w) M = fmaxf(M, sm[w][c * MW]);
+    float L = 0.f, f[KS];
+#pragma unroll
+    for (int w = 0; w < KS; ++w) {
+      const float mw = sm[w][c * MW];
+      f[w] = mw == -INFINITY ? 0.f : fexp_a(mw - M);
+      L += sm[w][c * MW + 1] * f[w];
+    }
+    const float inv = 1.0f / L;
+    float* orow = out + ((size_t)sidx * T + qi) * d + h * 64;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = (i / 4) * 8 + hh * 4 + (i % 4);
+      float a = 0.f, b = 0.f;
+#pragma unroll
+      for (int w = 0; w < KS; ++w) {
+        a += sm[w][c * MW + 2 + r] * f[w];
+        b += sm[w][c * MW + 2 + 32 + r] * f[w];
+      }
+      orow[r] = a * inv;
+      orow[32 + r] = b * inv;
+    }
+  }
+}
+
 void launch_attn_prefill(hipStream_t s, const float* qkv, int S, int T, int past, const float* kc, const float* vc,
                          int n_head, int n_pos, int d, float* out) {
+  if (d / n_head == 64 && (long)n_head * S < 256 && T + past >= 4 * FA_K) {
+    // few (sequence, head) pairs with long key ranges: split the keys over 4
+    // waves, 8 from 16 key blocks on (c3, 512 tokens of GPT-2 medium: 85.4k
+    // -> 96.9k tokens/s with 4, 5.25 -> 5.10-5.23 ms with 8; c2, 8 x 128
+    // tokens: 3.885 -> 3.82 ms with 4)
+    const int nqb = (T + FA_QW - 1) / FA_QW;
+    const dim3 grid(n_head, S, nqb);
+    if (T + past >= 16 * FA_K)
+      attn_prefill_ks_kernel<8><<<grid, 512, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
+    else
+      attn_prefill_ks_kernel<4><<<grid, 256, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
+    return;
+  }
   if (d / n_head == 64) {
-    const int nqb = (T + FA_QW * FA_W - 1) / (FA_QW * FA_W);
+    // 128 queries per workgroup where that gives two workgroups per CU, else
+    // 64 or 32 (a short batch of prompts would otherwise leave most CUs idle)
+    int fw = 4;
+    while (fw > 1 && (long)n_head * S * ((T + FA_QW * fw - 1) / (FA_QW * fw)) < 512) fw >>= 1;
+    const int nqb = (T + FA_QW * fw - 1) / (FA_QW * fw);
     dim3 grid(n_head, S, nqb);
-    attn_prefill_mfma_kernel<<<grid, FA_QW * 2 * FA_W, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
+    if (fw == 4)
+      attn_prefill_mfma_kernel<4><<<grid, 256, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
+    else if (fw == 2)
+      attn_prefill_mfma_kernel<2><<<grid, 128, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
+    else
+      attn_prefill_mfma_kernel<1><<<grid, 64, 0, s>>>(qkv, T, past, kc, vc, n_head, n_pos, d, nqb, out);
     return;
   }
   dim3 grid((T + PQ - 1) / PQ, n_head, S);

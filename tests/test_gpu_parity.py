@@ -459,6 +459,27 @@ def test_short_prompt_gemms_17_to_32_rows(O):
                             f"{n} new rows after {past}")
 
 
+def test_prefill_attention_key_split(O):
+    """Few long prompts run the prefill attention with the key range split
+    over the waves of a workgroup (attn_prefill_ks_kernel: 4 waves from 4 key
+    blocks of 32 on, 8 from 16 blocks on), each wave's (m, l, O) merged at the
+    end: rows of a prompt appended to a cache that already holds tokens
+    (past > 0, so the keys of the cached part enter every query's range) and
+    of a fresh one, against the oracle, every 37th row and the last 5."""
+    sd, sh, m = gpu_model("small")
+    om = O.OracleModel.from_shape(sd, sh, threads=min(16, os.cpu_count() or 1))
+    for past, n in ((0, 150), (40, 120), (100, 430)):
+        ids = synth.make_tokens(past + n, sh.vocab_size, stream=900 + n)
+        c, oc = m.new_cache(), om.new_cache()
+        if past:
+            m.forward_cached(ids[:past], c)
+            om.forward_cached(ids[:past], oc)
+        got = np.asarray(m.forward_cached(ids[past:], c))
+        ref = np.asarray(om.forward_cached(ids[past:], oc))
+        rows = sorted(set(range(0, n, 37)) | set(range(n - 5, n)))
+        assert_logits_close(got[rows], ref[rows], f"{n} new rows after {past}")
+
+
 def test_batched_forward_logits(O):
     sd, sh, m = gpu_model("mini")
     B, n = 3, 10
