@@ -765,16 +765,17 @@ __device__ __forceinline__ void gl_step(int kt, int nk, float (&lds)[2][GBM * 16
 // in acc[i][j] (32x32 blocks, MFMA output layout), to ws[z] as a raw partial
 // tile when ws is set, else with the epilogue (bias, gelu, residual; with kv
 // set, c_attn's k / v columns go into the cache at (sequence, head, past + t)).
-__device__ __forceinline__ void gl_epilogue(const floatx16 (&acc)[2][2], int lane, int m0, int n0, int wm, int wn,
+template <int I = 2, int J = 2>
+__device__ __forceinline__ void gl_epilogue(const floatx16 (&acc)[I][J], int lane, int m0, int n0, int wm, int wn,
                                             int z, const float* __restrict__ bias, float* __restrict__ C, long ldc,
                                             int M, int N, int epi, const KvDst& kv, int kv_T, int kv_past,
                                             float* __restrict__ ws) {
   if (ws != nullptr) {
     float* wz = ws + (size_t)z * M * N;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < I; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < J; ++j) {
         const int n = n0 + wn + j * 32 + (lane & 31);
         if (n >= N) continue;
 #pragma unroll
@@ -786,9 +787,9 @@ __device__ __forceinline__ void gl_epilogue(const floatx16 (&acc)[2][2], int lan
     return;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < I; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < J; ++j) {
       const int n = n0 + wn + j * 32 + (lane & 31);
       if (n >= N) continue;
       const float bv = bias ? bias[n] : 0.f;
@@ -898,6 +899,109 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const float* __restrict__
   }
 
   gl_epilogue(acc, lane, m0, n0, wm, wn, z, bias, C, ldc, M, N, epi, kv, kv_T, kv_past, ws);
+}
+
+// gemm_lds_kernel with 64 x 128 workgroup tiles (each wave 32 x 64, one A
+// group of 16 rows and two W groups per stage), for f32 GEMMs of at most 1024
+// rows: twice the workgroups of the 128 x 128 tiles, so fewer k splits and
+// reductions (c3's 512-row and c2's 1024-row prefill GEMMs: 5-25% faster
+// each, the split-k reduction included).
+constexpr int G64M = 64;
+template <int ST>
+__device__ __forceinline__ void g64_step(int kt, int nk, float (&la)[G64M * 16], float (&lw)[GBN * 16],
+                                         float (&na)[G64M * 16], float (&nw)[GBN * 16], const float* asrc,
+                                         const float* const (&wsrc)[2], int wave, const int (&aoff)[2],
+                                         const int (&woff)[2][2], floatx16 (&acc)[1][2]) {
+  if (kt + GL_NS - 2 < nk) gl_wait_barrier<(GL_NS - 2) * 3>();
+  else gl_wait_barrier<0>();
+  if (kt + GL_NS - 1 < nk) {
+    const int k = (kt + GL_NS - 1) * 16;
+    gl_dma16(asrc + k, &na[wave * 256]);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) gl_dma16(wsrc[q] + k, &nw[(2 * wave + q) * 256]);
+  }
+  float4 a[2], b[2][2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    a[c] = *reinterpret_cast<const float4*>(&la[aoff[c]]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b[j][c] = *reinterpret_cast<const float4*>(&lw[woff[j][c]]);
+  }
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const float4& av = a[st >> 2];
+    const int e = st & 3;
+    const float x = e == 0 ? av.x : e == 1 ? av.y : e == 2 ? av.z : av.w;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float4& bv = b[j][st >> 2];
+      const float y = e == 0 ? bv.x : e == 1 ? bv.y : e == 2 ? bv.z : bv.w;
+      acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[0][j], 0, 0, 0);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void gemm_lds64_kernel(const float* __restrict__ A, int lda,
+                                                         const float* __restrict__ W, const float* __restrict__ bias,
+                                                         float* __restrict__ C, long ldc, int M, int N, int K, int epi,
+                                                         int m_fast, KvDst kv, int kv_T, int kv_past, int ks,
+                                                         float* __restrict__ ws) {
+  __shared__ __attribute__((aligned(16))) float a0[G64M * 16], a1[G64M * 16], a2[G64M * 16], a3[G64M * 16];
+  __shared__ __attribute__((aligned(16))) float w0[GBN * 16], w1[GBN * 16], w2[GBN * 16], w3[GBN * 16];
+  static_assert(GL_NS == 4, "four stage arrays");
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 64;
+  const int nmb = (M + G64M - 1) / G64M, nnb = (N + GBN - 1) / GBN;
+  const int bid = blockIdx.x % (nmb * nnb), z = blockIdx.x / (nmb * nnb);
+  const int m0 = (m_fast ? bid % nmb : bid / nnb) * G64M, n0 = (m_fast ? bid / nmb : bid % nnb) * GBN;
+  const int nk = K / 16 / ks;
+  const int lr = lane >> 2;
+  const float* asrc;
+  {
+    const int row = wave * 16 + lr;
+    const int c = (lane & 3) ^ gl_swz(row);
+    asrc = A + (size_t)min(m0 + row, M - 1) * lda + c * 4 + (size_t)z * nk * 16;
+  }
+  const float* wsrc[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = (2 * wave + q) * 16 + lr;
+    const int c = (lane & 3) ^ gl_swz(row);
+    wsrc[q] = W + (size_t)min(n0 + row, N - 1) * K + c * 4 + (size_t)z * nk * 16;
+  }
+  auto issue = [&](int kt, float (&la)[G64M * 16], float (&lw)[GBN * 16]) {
+    gl_dma16(asrc + kt * 16, &la[wave * 256]);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) gl_dma16(wsrc[q] + kt * 16, &lw[(2 * wave + q) * 256]);
+  };
+  const int h = lane >> 5;
+  int aoff[2], woff[2][2];
+  {
+    const int ra = wm + (lane & 31);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) aoff[c] = ra * 16 + (((2 * h + c) ^ gl_swz(ra)) * 4);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rw = wn + 32 * j + (lane & 31);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) woff[j][c] = rw * 16 + (((2 * h + c) ^ gl_swz(rw)) * 4);
+    }
+  }
+  floatx16 acc[1][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[0][j][e] = 0.f;
+  issue(0, a0, w0);
+  issue(1, a1, w1);
+  issue(2, a2, w2);
+  for (int kt = 0; kt < nk; kt += GL_NS) {
+    g64_step<0>(kt, nk, a0, w0, a3, w3, asrc, wsrc, wave, aoff, woff, acc);
+    g64_step<1>(kt + 1, nk, a1, w1, a0, w0, asrc, wsrc, wave, aoff, woff, acc);
+    g64_step<2>(kt + 2, nk, a2, w2, a1, w1, asrc, wsrc, wave, aoff, woff, acc);
+    g64_step<3>(kt + 3, nk, a3, w3, a2, w2, asrc, wsrc, wave, aoff, woff, acc);
+  }
+  gl_epilogue<1, 2>(acc, lane, m0, n0, wm, wn, z, bias, C, ldc, M, N, epi, kv, kv_T, kv_past, ws);
 }
 
 // gemm_lds_kernel for bf16 weights (the f32 activations times W stored as
@@ -1481,11 +1585,27 @@ int gemm_splitk_factor(int M, int N, int K, int granule) {
   return best;
 }
 
+// k-splits of gemm_lds64_kernel (M <= 1024): as gemm_splitk_factor, over its
+// 64 x 128 output tiles (and, as there, none below 128 rows).
+static int gemm64_splitk_factor(int M, int N, int K) {
+  const int tiles = ((N + GBN - 1) / GBN) * ((M + G64M - 1) / G64M);
+  if (M < 128 || M > 1024 || tiles >= 192 || K % (16 * GL_NS) != 0) return 1;
+  const int nkt = K / 16;
+  int best = 1;
+  for (int sp = 2; sp <= 16; ++sp) {
+    if (nkt % (GL_NS * sp) != 0) continue;
+    best = sp;
+    if (tiles * sp >= 240) break;
+  }
+  return best;
+}
+
 size_t gemm_splitk_ws_floats(int M, int N, int K) {
-  // the larger of the two kernels' needs (which one runs depends on the
-  // weight type and alignment)
-  const int ks = std::max(std::max(gemm_splitk_factor(M, N, K, GL_NS), gemm_splitk_factor(M, N, K, 1)),
-                          std::max(skinny_splitk_factor(M, N, K), skinny_lds_splitk_factor(M, N, K)));
+  // the largest of the kernels' needs (which one runs depends on the weight
+  // type, the row count and alignment)
+  const int ks = std::max(std::max(std::max(gemm_splitk_factor(M, N, K, GL_NS), gemm_splitk_factor(M, N, K, 1)),
+                                   std::max(skinny_splitk_factor(M, N, K), skinny_lds_splitk_factor(M, N, K))),
+                          gemm64_splitk_factor(M, N, K));
   return ks > 1 ? (size_t)ks * M * N : 0;
 }
 
@@ -1503,6 +1623,16 @@ static void launch_gemm_lds(hipStream_t s, const float* A, int lda, const void* 
   const int nb = ((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM);
   int ks = gemm_splitk_factor(M, N, K, GL_NS);
   if (ks > 1 && (ws == nullptr || (size_t)ks * M * N > ws_floats)) ks = 1;
+  if (wtype == W_F32 && M <= 1024) {
+    // 64 x 128 tiles (gemm_lds64_kernel)
+    const int nb64 = ((N + GBN - 1) / GBN) * ((M + G64M - 1) / G64M);
+    int ks64 = gemm64_splitk_factor(M, N, K);
+    if (ks64 > 1 && (ws == nullptr || (size_t)ks64 * M * N > ws_floats)) ks64 = 1;
+    gemm_lds64_kernel<<<nb64 * ks64, 256, 0, s>>>(A, lda, static_cast<const float*>(W), bias, C, ldc, M, N, K, epi,
+                                                  N > M ? 1 : 0, kv, kv_T, kv_past, ks64, ks64 > 1 ? ws : nullptr);
+    if (ks64 > 1) splitk_reduce(s, ws, ks64, M, N, bias, C, ldc, epi, kv, kv_T, kv_past);
+    return;
+  }
   float* wsk = ks > 1 ? ws : nullptr;
   if (wtype == W_F32)
     gemm_lds_kernel<<<nb * ks, 256, 0, s>>>(A, lda, static_cast<const float*>(W), bias, C, ldc, M, N, K, epi,
