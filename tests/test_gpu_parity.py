@@ -360,6 +360,22 @@ def test_small_c1_logits_and_ids(O):
         assert_logits_close(m.forward_cached(tok, c), om.forward_cached(tok, oc), f"c1 step {t}")
 
 
+@pytest.mark.parametrize("name", ["mini", "small"])
+def test_persistent_step_repeatable(name):
+    """The persistent decode step sums in a fixed order everywhere (no
+    atomics on values, every exchange polled to completion), so identical
+    calls give identical tokens. Seeded sampling amplifies any logit
+    difference into a different draw, so it is the sensitive probe."""
+    _, sh, m = gpu_model(name)
+    prompt = synth.make_tokens(16, sh.vocab_size).tolist()
+    greedy = [m.generate_cached(prompt, 48, 0.0) for _ in range(4)]
+    assert all(g == greedy[0] for g in greedy), greedy
+    cfg = GenerationConfig.creative(48)
+    cfg.seed = 42
+    sampled = [m.generate_with_config(prompt, cfg) for _ in range(4)]
+    assert all(s_ == sampled[0] for s_ in sampled), sampled
+
+
 def test_small_batched_matches_single(O):
     sd, sh, m = gpu_model("small")
     B, n, steps = 8, 128, 256
