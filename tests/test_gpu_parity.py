@@ -360,7 +360,7 @@ def test_small_c1_logits_and_ids(O):
         assert_logits_close(m.forward_cached(tok, c), om.forward_cached(tok, oc), f"c1 step {t}")
 
 
-@pytest.mark.parametrize("name", ["mini", "small"])
+@pytest.mark.parametrize("name", ["mini", "small", "medium"])
 def test_persistent_step_repeatable(name):
     """The persistent decode step sums in a fixed order everywhere (no
     atomics on values, every exchange polled to completion), so identical
