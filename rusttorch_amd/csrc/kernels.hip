@@ -1532,17 +1532,19 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= (long)M * N) return;
   const int m = (int)(i / N), n = (int)(i - (long)m * N);
-  // the partials in flight eight at a time, summed in z order
-  float v = ws[i];
-  int z = 1;
-  for (; z + 8 <= ks; z += 8) {
-    float t[8];
+  // every partial of a chunk of 16 in flight at once (the splits never
+  // exceed 16, so one round trip), summed in z order
+  const size_t MN = (size_t)M * N;
+  float v = 0.f;
+  for (int z0 = 0; z0 < ks; z0 += 16) {
+    float t[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) t[u] = ws[(size_t)(z + u) * M * N + i];
+    for (int u = 0; u < 16; ++u) t[u] = z0 + u < ks ? ws[(size_t)(z0 + u) * MN + i] : 0.f;
+    if (z0 == 0) v = t[0];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v += t[u];
+    for (int u = 0; u < 16; ++u)
+      if ((z0 > 0 || u > 0) && z0 + u < ks) v += t[u];
   }
-  for (; z < ks; ++z) v += ws[(size_t)z * M * N + i];
   const float bv = bias ? bias[n] : 0.f;
   if (kv.k != nullptr && n >= kv.d) {
     const int which = n >= 2 * kv.d, cc = n - kv.d - which * kv.d;
