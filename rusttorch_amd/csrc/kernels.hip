@@ -465,9 +465,19 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ l
   const int row = blockIdx.y;
   const float* p = logits + (size_t)row * ld;
   unsigned long long best = 0ull;
-  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < V; j += gridDim.x * blockDim.x) {
-    const unsigned long long k = argmax_key(p[j], (uint32_t)j);
-    best = k > best ? k : best;
+  // eight loads of a thread in flight at once (the packed keys make the
+  // reduction order-free)
+  const int stride = gridDim.x * blockDim.x;
+  for (int j0 = blockIdx.x * blockDim.x + threadIdx.x; j0 < V; j0 += 8 * stride) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = j0 + u * stride < V ? p[j0 + u * stride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u * stride;
+      const unsigned long long k = j < V ? argmax_key(v[u], (uint32_t)j) : 0ull;
+      best = k > best ? k : best;
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
