@@ -90,16 +90,33 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
   const int pos = *pos_dev;
   float v[8];  // d <= 2048
   float s = 0.f;
+  // every load of the row in flight at once (branch-free: lanes past the
+  // row's end re-read its last element and drop it), then the stores
+  float w[8], pe[8], gk[8];
+  if (wtype == W_F32) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = static_cast<const float*>(wte)[tok * d + min(tid + 256 * i, d - 1)];
+  } else {
+    uint32_t wb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wb[i] = static_cast<const uint16_t*>(wte)[tok * d + min(tid + 256 * i, d - 1)];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = __uint_as_float(wb[i] << 16);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int k = min(tid + 256 * i, d - 1);
+    pe[i] = wpe[(long)pos * d + k];
+    gk[i] = g[k];
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int k = tid + 256 * i;
     v[i] = 0.f;
     if (k < d) {
-      const float w = wtype == W_F32 ? static_cast<const float*>(wte)[tok * d + k]
-                                     : __uint_as_float((uint32_t)static_cast<const uint16_t*>(wte)[tok * d + k] << 16);
-      v[i] = w + wpe[(long)pos * d + k];
+      v[i] = w[i] + pe[i];
       x[(long)b * d + k] = v[i];
-      xg[xt_index(b, k, gridDim.x, tk)] = v[i] * g[k];
+      xg[xt_index(b, k, gridDim.x, tk)] = v[i] * gk[i];
       s += v[i];
     }
   }
