@@ -141,25 +141,36 @@ constexpr int LNW_MAXC = 8;  // 16-byte chunks per lane: d <= 64 * 4 * 8
 // full-wave sum in every lane on DPP and permlane swaps (no LDS traffic)
 __device__ __forceinline__ float wave_sum_dpp(float v) { return xor32_sum_k(xor16_sum_k(row16_sum_k(v))); }
 
+template <int NU>
 __global__ __launch_bounds__(256) void layernorm_wave_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                              const float* __restrict__ b, float eps, int rows, int d,
                                                              float* __restrict__ out) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= rows) return;  // wave-uniform
   const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * d);
-  const int nc = d >> 2;
-  float4 v[LNW_MAXC];
+  const int nc = d >> 2;  // 16-byte chunks of the row, NU per lane at most
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  const float4* b4 = reinterpret_cast<const float4*>(b);
+  // the row, the gain and the bias in flight together (branch-free: chunks
+  // past the row's end re-read its last chunk and are dropped)
+  float4 v[NU], gv[NU], bv[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int ch = min(lane + 64 * u, nc - 1);
+    v[u] = xr[ch];
+    gv[u] = w4[ch];
+    bv[u] = b4[ch];
+  }
   float sum = 0.f;
 #pragma unroll
-  for (int u = 0; u < LNW_MAXC; ++u) {
-    const int ch = lane + 64 * u;
-    v[u] = ch < nc ? xr[ch] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int u = 0; u < NU; ++u) {
+    if (lane + 64 * u >= nc) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     sum += (v[u].x + v[u].y) + (v[u].z + v[u].w);
   }
   const float mean = wave_sum_dpp(sum) / (float)d;
   float sq = 0.f;
 #pragma unroll
-  for (int u = 0; u < LNW_MAXC; ++u) {
+  for (int u = 0; u < NU; ++u) {
     if (lane + 64 * u < nc) {
       const float a = v[u].x - mean, bb = v[u].y - mean, cc = v[u].z - mean, dd = v[u].w - mean;
       sq += (a * a + bb * bb) + (cc * cc + dd * dd);
@@ -168,13 +179,11 @@ __global__ __launch_bounds__(256) void layernorm_wave_kernel(const float* __rest
   const float var = wave_sum_dpp(sq) / (float)d;
   const float inv_std = 1.0f / sqrtf(var + eps);
   float4* orow = reinterpret_cast<float4*>(out + (size_t)row * d);
-  const float4* w4 = reinterpret_cast<const float4*>(w);
-  const float4* b4 = reinterpret_cast<const float4*>(b);
 #pragma unroll
-  for (int u = 0; u < LNW_MAXC; ++u) {
+  for (int u = 0; u < NU; ++u) {
     const int ch = lane + 64 * u;
     if (ch < nc) {
-      const float4 g = w4[ch], bi = b4[ch];
+      const float4 g = gv[u], bi = bv[u];
       orow[ch] = make_float4((v[u].x - mean) * inv_std * g.x + bi.x, (v[u].y - mean) * inv_std * g.y + bi.y,
                              (v[u].z - mean) * inv_std * g.z + bi.z, (v[u].w - mean) * inv_std * g.w + bi.w);
     }
@@ -183,9 +192,19 @@ __global__ __launch_bounds__(256) void layernorm_wave_kernel(const float* __rest
 
 void launch_layernorm(hipStream_t s, const float* x, const float* w, const float* b, float eps, int rows, int d,
                       float* out) {
-  if (d % 4 == 0 && d <= 256 * LNW_MAXC)
-    layernorm_wave_kernel<<<(rows + 3) / 4, 256, 0, s>>>(x, w, b, eps, rows, d, out);
-  else
+  if (d % 4 == 0 && d <= 256 * LNW_MAXC) {
+    const dim3 grid((rows + 3) / 4);
+    switch ((d + 255) / 256) {
+      case 1: layernorm_wave_kernel<1><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+      case 2: layernorm_wave_kernel<2><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+      case 3: layernorm_wave_kernel<3><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+      case 4: layernorm_wave_kernel<4><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+      case 5: layernorm_wave_kernel<5><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+      case 6: layernorm_wave_kernel<6><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+      case 7: layernorm_wave_kernel<7><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+      default: layernorm_wave_kernel<8><<<grid, 256, 0, s>>>(x, w, b, eps, rows, d, out); break;
+    }
+  } else
     layernorm_kernel<<<rows, 256, 0, s>>>(x, w, b, eps, d, out);
 }
 
