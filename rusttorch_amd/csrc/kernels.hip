@@ -521,8 +521,15 @@ void launch_argmax(hipStream_t s, const float* logits, long ld, int rows, int V,
 __global__ __launch_bounds__(256) void finalize_kernel(int B, unsigned long long* keys, uint32_t* token,
                                                        uint32_t* ids_out, int ld_ids, int* pos_dev, int* step_dev,
                                                        unsigned* epoch) {
+  // the counters and the keys are read together (one round trip); thread 0
+  // advances the counters once every thread has read *step_dev
   const int step = *step_dev;
-  __syncthreads();
+  int pos = 0;
+  unsigned ep = 0u;
+  if (threadIdx.x == 0) {
+    pos = *pos_dev;
+    if (epoch) ep = *epoch;
+  }
   for (int b = threadIdx.x; b < B; b += blockDim.x) {
     const uint32_t t = argmax_key_index(keys[b]);
     token[b] = t;
@@ -531,9 +538,9 @@ __global__ __launch_bounds__(256) void finalize_kernel(int B, unsigned long long
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    *pos_dev += 1;
+    *pos_dev = pos + 1;
     *step_dev = step + 1;
-    if (epoch) *epoch += 1u;
+    if (epoch) *epoch = ep + 1u;
   }
 }
 
