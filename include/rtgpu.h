@@ -127,19 +127,27 @@ rtg_result rtg_cache_read(const rtg_cache* cache, size_t layer, size_t head, siz
 /* Gpt2Model::forward, gpt2.rs:269-304: logits_out[n * vocab_size]. */
 rtg_result rtg_forward(const rtg_model* model, const uint32_t* ids, size_t n, float* logits_out);
 /* Gpt2Model::forward_cached, gpt2.rs:358-399: logits_out[n * vocab_size]
- * (may be NULL to skip the device-to-host copy). The cache must have batch 1. */
+ * (may be NULL to skip the device-to-host copy). The cache must have batch 1
+ * and belong to model. One new token (n == 1) runs the persistent decode
+ * step that generate_cached runs per token, where the model's shape has one;
+ * more tokens run the prefill kernels. */
 rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
                               float* logits_out);
 /* forward_cached without device allocation. No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
- * arguments, kernels and results as rtg_forward_cached, but the activations
- * and logits of the pass live in a fixed 16 MiB scratch array per device
- * inside the library instead of the cache's work buffers, and nothing is
- * allocated. Limit: n * (10 * n_embd + vocab_size) floats (each of the six
- * parts rounded up to 64) must fit in 16 MiB, e.g. n <= 72 for GPT-2 small;
- * a larger n returns an error. All calls on one device share the array:
- * calls that overlap on one device race. */
+ * arguments as rtg_forward_cached and the kernels of its prefill path (for
+ * n >= 2 the same results bit for bit; for n == 1 rtg_forward_cached runs
+ * the persistent decode step instead, and the two agree within the logits
+ * tolerance), but the activations and logits of the pass live in a fixed
+ * 16 MiB scratch array per device inside the library instead of the cache's
+ * work buffers, and nothing is allocated. Limit: n * (10 * n_embd +
+ * vocab_size) floats (each of the six parts rounded up to 64) must fit in
+ * 16 MiB, e.g. n <= 72 for GPT-2 small, n <= 63 for XL; a larger n returns
+ * an error. The prefill GEMMs' split-k partials take what is left of the
+ * array; where they do not fit the GEMMs run unsplit. All calls on one
+ * device share the array and take turns on it (a per-device lock held until
+ * the call's stream has drained). The cache must belong to model. */
 rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
                                       float* logits_out);
 /* Gpt2Model::generate (uncached, sliding window), gpt2.rs:311-346.

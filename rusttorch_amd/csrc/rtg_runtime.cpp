@@ -564,6 +564,32 @@ static void forward_cached_impl(rtg_cache* c, const uint32_t* ids, size_t n, flo
   const size_t B = c->batch, V = m->cfg.vocab_size;
   ensure_rows(c, B * n);
   ensure_logits(c, B * n);
+  if (n == 1 && B == 1 && persistent_supported(m->pplan, 1)) {
+    // one new token at batch 1: the persistent decode step, the kernel
+    // generate_cached runs per token; its token is read from token_dev at
+    // position *pos_dev = past, its logits land in c->logits
+    if (!c->pstate) {
+      c->pstate = persistent_state_create(m->pplan, c->k, c->v, 1, c->token_dev, c->pos_dev, c->logits, c->keys,
+                                          c->ids_dev, c->step_dev);
+      destroy_graph(c);
+    }
+  }
+  if (n == 1 && B == 1 && c->pstate) {
+    std::lock_guard<std::mutex> plock(persistent_launch_lock(m->device));
+    HIPX(hipMemcpyAsync(c->token_dev, ids, 4, hipMemcpyHostToDevice, c->stream));
+    set_counters(c, (int)c->len, 0);
+    HIPX(persistent_decode_step(c->pstate, c->stream, /*cooperative=*/false));
+    if (logits_out) HIPX(hipMemcpyAsync(logits_out, c->logits, V * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPX(hipStreamSynchronize(c->stream));
+    unsigned e = 0;
+    HIPX(hipMemcpy(&e, persistent_err(c->pstate), 4, hipMemcpyDeviceToHost));
+    if (e) {
+      HIPX(hipMemset(persistent_err(c->pstate), 0, 4));
+      throw HipError{fmt("persistent decode step timed out waiting for a peer (code %u)", e)};
+    }
+    c->len += 1;
+    return;
+  }
   if (n == 1 && B >= 2 && !c->pstate && batched_ok(m, B)) {
     // one new token per sequence: the batched decode step (the same kernels
     // generate_cached_batched replays), its token read from token_dev at
@@ -1060,6 +1086,7 @@ rtg_result rtg_cache_read(const rtg_cache* c, size_t layer, size_t head, size_t 
 rtg_result rtg_forward_cached_batched(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
                                       float* logits_out) {
   if (!model || !cache) return err("null argument");
+  if (cache->m != model) return err("the cache belongs to another model");
   std::string e = check_cached(model, cache->len, ids, n);
   if (e.empty() && cache->batch > 1) e = check_ids(model, ids, n * cache->batch);
   if (!e.empty()) return err(e);
@@ -1081,6 +1108,8 @@ rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const ui
 rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
                                       float* logits_out) {
   if (!model || !cache || (n && !ids)) return err("null argument");
+  // the pass runs cache->m's kernels on buffers sized from model's shape
+  if (cache->m != model) return err("rtg_forward_cached_noalloc: the cache belongs to another model");
   if (cache->batch != 1) return err("rtg_forward_cached_noalloc needs a batch-1 cache");
   std::string e = check_cached(model, cache->len, ids, n);
   if (!e.empty()) return err(e);
@@ -1097,14 +1126,21 @@ rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, 
                          std::make_pair(d, 4 * d)})
     pw = std::max(pw, gemm_splitk_ws_floats((int)n, (int)nk.first, (int)nk.second));
   pw = align_up(pw, 64);
-  const size_t need = 3 * pd + p3 + p4 + pv + pw;
+  const size_t need = 3 * pd + p3 + p4 + pv;
   if (need > kScratchFloats)
     return err(fmt("rtg_forward_cached_noalloc: %zu new tokens need %zu bytes of scratch; it holds %zu", n,
                    need * 4, kScratchFloats * 4));
+  // where the GEMMs' split-k partials do not fit beside the activations the
+  // GEMMs run unsplit (the same sums in another order), so the limit is
+  // exactly the activations' size and grows monotonically with n
+  if (need + pw > kScratchFloats) pw = 0;
   try {
     hipError_t he = hipSuccess;
     float* sp = scratch_device_ptr(model->device, &he);
     HIPX(he);
+    // every call on this device shares the array: one pass at a time (the
+    // call has drained its stream when it returns)
+    std::lock_guard<std::mutex> slock(scratch_lock(model->device));
     // Nothing here has to start at zero: every kernel of the pass writes its
     // output rows in full before they are read (the residual epilogues add
     // into x after the embedding has written it).

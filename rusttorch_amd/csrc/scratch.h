@@ -5,15 +5,23 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include <mutex>
+
 namespace rtg {
 
 // 16 MiB: GPT-2 small takes (10 d + V) floats per new token (x, ln, att:
-// d each; qkv 3d; h 4d; one logits row), so 72 tokens fit; XL 63.
+// d each; qkv 3d; h 4d; one logits row), so 72 tokens fit; XL 63. The
+// prefill GEMMs' split-k partials use what is left, else the GEMMs run
+// unsplit.
 constexpr size_t kScratchFloats = (size_t)4 << 20;
 
 // Device address of `device`'s copy of the array (looked up once per device
 // with hipGetSymbolAddress, with that device current; the current device is
 // restored afterwards). Null with *err set on failure.
 float* scratch_device_ptr(int device, hipError_t* err);
+
+// Held by a call from its first use of `device`'s array until its stream has
+// drained, so that calls from several threads take turns on the array.
+std::mutex& scratch_lock(int device);
 
 }  // namespace rtg

@@ -4,7 +4,7 @@
 // device symbol: passing it to a kernel would fault. Host code therefore uses
 // the address hipGetSymbolAddress returns for the device, never the name.
 // Every device holds its own copy of the array until the process ends; calls
-// on one device share it (overlapping calls on one device race).
+// on one device share it and take scratch_lock(device) for the whole pass.
 #include "scratch.h"
 
 #include <mutex>
@@ -40,6 +40,11 @@ float* scratch_device_ptr(int device, hipError_t* err) {
   }
   *err = hipSuccess;
   return ptrs[device];
+}
+
+std::mutex& scratch_lock(int device) {
+  static std::mutex locks[64];
+  return locks[(unsigned)device % 64u];
 }
 
 }  // namespace rtg
