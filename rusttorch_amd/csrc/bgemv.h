@@ -46,6 +46,14 @@ struct BgemvArgs {
   const float* ln_part;
   int ln_groups, ln_cols;
   float eps;
+  // Centring of the folded LayerNorm: X holds (x - cen_in[m]) * g (the
+  // producer subtracted that centre), so the epilogue computes
+  // inv_std * (acc - (mean - cen_in[m]) * ln_s[n]) and no term carries the
+  // row's full mean (null: centre 0). cen_out[m] receives the row's exact
+  // mean (written once, by the workgroup of panel group 0): the centre of
+  // the next residual producer.
+  const float* cen_in;
+  float* cen_out;
   // Residual epilogue only: writes those partials for the rows it wrote,
   // stats_part[g][m] for its panel groups g (plan.groups * 32 floats), with
   // groups of 16 * plan.npw columns; with xg set, also y * g_next[n] to xg in
@@ -54,6 +62,8 @@ struct BgemvArgs {
   float* stats_part;
   float* xg;
   const float* g_next;
+  // with xg: (y - xg_cen[m]) * g_next[n] is written instead (null: centre 0)
+  const float* xg_cen;
   // LM head: per-row packed argmax keys (gpt2.rs:858-868), updated with a
   // device-scope atomic max (zero before; the step's finalize resets them).
   unsigned long long* keys;
@@ -81,12 +91,13 @@ bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a);
 size_t bgemv_work_floats(const BgemvPlan& pl);
 bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a);
 // Decode embedding x[r] = wte[token[r]] + wpe[*pos_dev] of rows r < rows,
-// x[r] * g in the GEMV input layout to xg (xt_index(r, k, rows, TK of wtype):
-// the input of the LayerNorm-folded GEMV that follows) and their LayerNorm
-// statistics partials as one group of width d: part[r] = (mean, M2) (the
-// ln_part of the following GEMV, ln_groups = 1). d <= 2048.
+// (x[r] - mean_r) * g in the GEMV input layout to xg (xt_index(r, k, rows,
+// TK of wtype): the input of the LayerNorm-folded GEMV that follows, centred
+// on the row's mean, cen[r] = mean_r) and their LayerNorm statistics
+// partials as one group of width d: part[r] = (mean, M2) (the ln_part of the
+// following GEMV, ln_groups = 1). d <= 2048.
 bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
                         const int* pos_dev, int rows, int d, float* x, float* part, const float* g,
-                        float* xg);
+                        float* xg, float* cen);
 
 }  // namespace rtg

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
                                                           const uint32_t* __restrict__ token,
                                                           const int* __restrict__ pos_dev, int d,
                                                           float* __restrict__ x, float* __restrict__ part,
-                                                          const float* __restrict__ g, float* __restrict__ xg) {
+                                                          const float* __restrict__ g, float* __restrict__ xg,
+                                                          float* __restrict__ cen) {
   __shared__ float red[4];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int tk = wtype == W_F32 ? 16 : 32;  // xg in the GEMV input layout
@@ -116,7 +117,6 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
     if (k < d) {
       v[i] = w[i] + pe[i];
       x[(long)b * d + k] = v[i];
-      xg[xt_index(b, k, gridDim.x, tk)] = v[i] * gk[i];
       s += v[i];
     }
   }
@@ -137,9 +137,18 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const void* __restrict
     q += tid + 256 * i < d ? t * t : 0.f;
   }
   q = block_sum(q);
+  // the GEMV input centred on the row's own mean: (x - mean) * g, so that the
+  // folded LayerNorm of the next GEMV subtracts no large mean (cen[b] = the
+  // centre used)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int k = tid + 256 * i;
+    if (k < d) xg[xt_index(b, k, gridDim.x, tk)] = (v[i] - mean) * gk[i];
+  }
   if (tid == 0) {
     part[2 * b] = mean;
     part[2 * b + 1] = q;
+    cen[b] = mean;
   }
 }
 
@@ -194,6 +203,8 @@ bool bgemv_args_ok(const BgemvPlan& pl, const BgemvArgs& a) {
                  (a.ln_groups - 1) * a.ln_cols >= a.K || a.ln_groups * a.ln_cols < a.K))
     return false;
   if (a.stats_part && a.epi != EPI_BIAS_RESID) return false;
+  if ((a.cen_in || a.cen_out) && !a.ln_g) return false;
+  if (a.xg_cen && !a.xg) return false;
   return true;
 }
 
@@ -233,9 +244,9 @@ bool launch_bgemv(hipStream_t s, const BgemvPlan& pl, BgemvArgs a) {
 
 bool launch_embed_stats(hipStream_t s, const void* wte, int wtype, const float* wpe, const uint32_t* token,
                         const int* pos_dev, int rows, int d, float* x, float* part, const float* g,
-                        float* xg) {
+                        float* xg, float* cen) {
   if (d > 2048 || d % (wtype == W_F32 ? 16 : 32) != 0) return false;
-  embed_stats_kernel<<<rows, 256, 0, s>>>(wte, wtype, wpe, token, pos_dev, d, x, part, g, xg);
+  embed_stats_kernel<<<rows, 256, 0, s>>>(wte, wtype, wpe, token, pos_dev, d, x, part, g, xg, cen);
   return hipGetLastError() == hipSuccess;
 }
 

@@ -341,8 +341,14 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
     __syncthreads();  // the LDS partials are free again once the epilogue threads read them
     return;
   }
-  float mean = 0.f, inv_std = 0.f;
-  if constexpr (LNG) row_stats_merge(a, lnp, mean, inv_std);
+  float mean = 0.f, inv_std = 0.f, mc = 0.f;
+  if constexpr (LNG) {
+    row_stats_merge(a, lnp, mean, inv_std);
+    // the input was centred on cen_in[m]: only the drift of the mean remains
+    mc = mean - (a.cen_in && m < a.M ? a.cen_in[m] : 0.f);
+    if (a.cen_out && g == 0 && (tid & 15) == 0 && m < a.M) a.cen_out[m] = mean;
+  }
+  const float xc = a.xg_cen && m < a.M ? a.xg_cen[m] : 0.f;
   if (!early) {
 #pragma unroll
     for (int j = 0; j < NPW; ++j) eo[j] = load_epi(a, m, (g * NPW + j) * 16 + (tid & 15), LNG);
@@ -358,9 +364,9 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
     y[j] = 0.f;
     if (valid[j]) {
       float t = v[j];
-      if constexpr (LNG) t = inv_std * (t - mean * eo[j].ln_s);
+      if constexpr (LNG) t = inv_std * (t - mc * eo[j].ln_s);
       y[j] = store_out(a, m, n, t, eo[j], pos, TK);
-      if (a.xg) a.xg[xt_index(m, n, a.M, TK)] = y[j] * eo[j].g_next;
+      if (a.xg) a.xg[xt_index(m, n, a.M, TK)] = (y[j] - xc) * eo[j].g_next;
       if (a.keys) {
         const u64 k = argmax_key(y[j], (uint32_t)n);
         best = k > best ? k : best;

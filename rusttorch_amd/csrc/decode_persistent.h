@@ -38,9 +38,12 @@ void persistent_state_destroy(PersistentState* s);
 // and finishes the step itself (the finalize kernel's work): the argmax token
 // goes to *token_dev and ids_dev[*step_dev], *pos_dev and *step_dev advance
 // by one, the packed argmax key is cleared.
+// pos is the position of the token the step consumes (the value *pos_dev
+// holds when the step runs), or -1 if unknown: it selects between the
+// tiled step (short contexts, where built) and the row-split step.
 // The caller must hold persistent_launch_lock(device) from the first step it
 // enqueues until its stream has drained.
-hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative);
+hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative, int pos);
 // One lock per device: persistent steps of two streams in flight at once could
 // each hold part of the CUs and wait on workgroups that cannot start.
 std::mutex& persistent_launch_lock(int device);

@@ -11,6 +11,7 @@
 
 #include "decode_persistent.h"
 #include "decode_persistent_kernel.h"
+#include "decode_tile.h"
 
 namespace rtg {
 namespace pk {
@@ -77,11 +78,14 @@ struct PersistentPlan {
   pk::LayerPtrs* layers_dev = nullptr;
   void* zeros = nullptr;
   float* fold = nullptr;  // folded LayerNorm constants (LayerPtrs::sq etc., Params::sl/cl)
+  TilePlan* tile = nullptr;  // the tiled step (decode_tile_kernel.h) for short contexts, where built
 };
 
 struct PersistentState {
   PersistentPlan* plan;
   pk::Params p;
+  tk::TParams tp{};  // the tiled step's parameters (same decode state, its own exchange words)
+  pk::u64* ttags = nullptr;
   pk::u64* tags = nullptr;
   unsigned* epoch = nullptr;
   unsigned* err = nullptr;
@@ -150,6 +154,11 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   p.o_x3 = p.o_h + region(4 * d);
   p.lw = p.o_x3 + region(d);
   pl->kernel = fn;
+  // The tiled step is opt-in: measured slower than the row-split step at c1
+  // (253.6 against 209 us per token), it is kept for its exact block-centred
+  // LayerNorm and as the measured alternative exchange structure.
+  const char* te = getenv("RTG_TILE_STEP");
+  if (tile_supported(d, H, V, w.wtype, cus) && te && te[0] == '1') pl->tile = tile_plan_create(w);
   return pl;
 }
 
@@ -158,6 +167,7 @@ void persistent_plan_destroy(PersistentPlan* pl) {
   if (pl->layers_dev) hipFree(pl->layers_dev);
   if (pl->zeros) hipFree(pl->zeros);
   if (pl->fold) hipFree(pl->fold);
+  tile_plan_destroy(pl->tile);
   delete pl;
 }
 
@@ -211,6 +221,31 @@ PersistentState* persistent_state_create(PersistentPlan* pl, float* kcache, floa
   p.ids_out = ids_dev;
   p.step = step_dev;
   p.done = s->done;
+  if (const TilePlan* tp = pl->tile) {
+    // the tiled step shares the decode state (token, position, epoch, keys,
+    // error word) and has its own exchange words; tag 0 never matches
+    if (hipMalloc(&s->ttags, tp->tag_words * 8) != hipSuccess ||
+        hipMemset(s->ttags, 0, tp->tag_words * 8) != hipSuccess) {
+      persistent_state_destroy(s);
+      return nullptr;
+    }
+    tk::TParams& t = s->tp;
+    t = tp->base;
+    t.kc = kcache;
+    t.vc = vcache;
+    t.token = token_dev;
+    t.pos = pos_dev;
+    t.ids_out = ids_dev;
+    t.step = step_dev;
+    t.done = s->done;
+    t.epoch = s->epoch;
+    t.tag = s->ttags;
+    t.logits = logits;
+    t.keys = keys;
+    t.err = s->err;
+    t.trace = p.trace;
+    t.dummy = pl->zeros;
+  }
   return s;
 }
 
@@ -221,6 +256,7 @@ void persistent_state_destroy(PersistentState* s) {
   if (s->err) hipFree(s->err);
   if (s->trace) hipFree(s->trace);
   if (s->done) hipFree(s->done);
+  if (s->ttags) hipFree(s->ttags);
   delete s;
 }
 
@@ -240,7 +276,11 @@ void persistent_dump_trace(PersistentState* s) {
 unsigned* persistent_epoch(PersistentState* s) { return s ? s->epoch : nullptr; }
 unsigned* persistent_err(PersistentState* s) { return s ? s->err : nullptr; }
 
-hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative) {
+hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool cooperative, int pos) {
+  // the tiled step where the plan has one and the context fits its LDS
+  // windows; both kernels keep the same decode state, so steps may alternate
+  if (s->plan->tile && s->ttags && pos >= 0 && pos + 1 <= tile_max_len())
+    return tile_decode_step(s->plan->tile, s->tp, stream, cooperative);
   void* args[] = {&s->p};
   const void* fn = s->plan->kernel;
   if (cooperative) return hipLaunchCooperativeKernel(fn, dim3(pk::G), dim3(pk::NTHREADS), args, 0, stream);

@@ -80,7 +80,10 @@ struct LayerPtrs {
   const float *bqkv, *baproj, *bfc, *bmproj, *ln1w, *ln1b, *ln2w, *ln2b;
   // LayerNorm folded into the following GEMV (computed once at load time):
   // for output row r, s[r] = sum_k W[r][k] g[k] and c[r] = bias[r] +
-  // sum_k W[r][k] b[k], so LN(x) @ W + bias = inv_std * (W.(x*g) - mean * s) + c.
+  // sum_k W[r][k] b[k], so with the GEMV input centred on a value c0 known
+  // ahead (the mean of the previous LayerNorm's input),
+  // LN(x) @ W + bias = inv_std * (W.((x - c0) g) - (mean - c0) s) + c:
+  // only the drift of the mean between two LayerNorms is subtracted.
   const float *sq, *cq, *sf, *cf;
 };
 
@@ -176,7 +179,7 @@ template <int D>
 struct Smem {
   float in_vec[2][4 * D];  // GEMV input, double-buffered by phase parity
   float xraw[D];           // residual input of the current layer
-  float x2raw[D];          // residual after attention
+  float x2raw[2][D];       // residual after attention, by layer parity (read one layer later as a centre)
   float part[PART_MAX];
   float stage[CMAX * ITEM_WORDS];  // a chunked head's items, on the workgroup that merges them
   float kv_k[KVS * HD], kv_v[KVS * HD];  // K/V rows [j0, j0 + KVS) of this workgroup's item
@@ -550,6 +553,16 @@ __device__ __forceinline__ int slot_of(int i) {
   return (i / RPW) * SW + i % RPW;
 }
 
+// Mean of the D floats x (LDS) on one wave: a lane's D / 64 values summed in
+// order, then the fixed wave reduction; every wave gets the same value.
+template <int D>
+__device__ __forceinline__ float lds_mean(const float* x, int lane) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < D / 64; ++k) s += x[lane + 64 * k];
+  return wave_sum_all(s) / (float)D;
+}
+
 // All glue lanes fetch the n tagged words of an exchange into dst: every
 // word is read with a coherent load (never a stale line of this XCD's L2)
 // and stale words are re-read until their tags equal the step's epoch. The
@@ -563,11 +576,19 @@ __device__ __forceinline__ int slot_of(int i) {
 // staggered rounds in flight per word: 252 µs). With SCALE,
 // dst2[i] = word * g[i] as well (the LayerNorm gain applied to a GEMV input
 // whose LayerNorm is folded).
-template <int RPW, int SW, int NMAX, bool SCALE = false>
+// With SCALE the GEMV input is also centred: dst2[i] = (word - c0) * g[i],
+// c0 = the mean of the D floats at cen_src (the previous LayerNorm's input,
+// in LDS once *rdy >= rdy_n), computed by every glue wave alike while its
+// first polling round is in flight, and returned in *c0.
+template <int RPW, int SW, int NMAX, bool SCALE = false, int D = 0>
 __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, float* dst, int gl, unsigned* err,
-                                           float* dst2 = nullptr, const float* g = nullptr) {
+                                           float* dst2 = nullptr, const float* g = nullptr,
+                                           const float* cen_src = nullptr, unsigned* rdy = nullptr,
+                                           unsigned rdy_n = 0, float* c0 = nullptr) {
   constexpr int NG = NGLUE * 64;
   constexpr int NW = (NMAX + NG - 1) / NG;
+  static_assert(!SCALE || (NMAX >= D && D % 64 == 0), "a centred fetch is one polling round over D words");
+  float cen = 0.f;
   for (int base = 0; base < n; base += NW * NG) {
     float gv[NW];
     if constexpr (SCALE) {
@@ -582,6 +603,11 @@ __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, 
     for (int k = 0; k < NW; ++k) {
       const int i = base + gl + k * NG;
       w[k] = i < n ? tload(src + slot_of<RPW, SW>(i)) : ((u64)tag << 32);
+    }
+    if constexpr (SCALE) {
+      lds_wait_ge(rdy, rdy_n, err);
+      cen = lds_mean<D>(cen_src, gl & 63);
+      *c0 = cen;
     }
     unsigned spins = 0;
     for (;;) {
@@ -606,7 +632,7 @@ __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, 
       if (i < n) {
         const float v = __uint_as_float((unsigned)w[k]);
         dst[i] = v;
-        if constexpr (SCALE) dst2[i] = v * gv[k];
+        if constexpr (SCALE) dst2[i] = (v - cen) * gv[k];
       }
     }
   }
@@ -794,16 +820,19 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   // embedding (gpt2.rs:377-384): every workgroup computes x0 itself, each
   // glue wave a third of it
   if (leader) PK_TRACE(p, 0, lane);
+  float c0q = 0.f;  // centre of the c_attn input (see LayerPtrs)
   {
     const float* g1 = PK_C(LayerPtrs, p.layers)[0].ln1w;
     for (int i = gl; i < D; i += NGLUE * 64) {
       float w;
       if (C::WT == W_F32) w = PK_G(float, p.wte)[(long)tok * D + i];
       else w = __uint_as_float((uint32_t)PK_G(uint16_t, p.wte)[(long)tok * D + i] << 16);
-      const float x = w + PK_G(float, p.wpe)[(long)pos * D + i];
-      sm.xraw[i] = x;
-      sm.in_vec[1][i] = x * PK_G(float, g1)[i];
+      sm.xraw[i] = w + PK_G(float, p.wpe)[(long)pos * D + i];
     }
+    // layer 0's input centred on its own mean (no previous LayerNorm)
+    glue_barrier(sm, gen, lane, p.err);
+    c0q = lds_mean<D>(sm.xraw, lane);
+    for (int i = gl; i < D; i += NGLUE * 64) sm.in_vec[1][i] = (sm.xraw[i] - c0q) * PK_G(float, g1)[i];
     glue_input_done(sm, PH_QKV, lane);
   }
   const int item = wg < items ? wg : -1;
@@ -837,9 +866,10 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         sr = PK_G(float, LP.sq)[row0 + lane];
         cr = PK_G(float, LP.cq)[row0 + lane];
       }
-      if (l > 0) {
-        glue_fetch<GM::RPW, GM::SW, D, true>(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err,
-                                          sm.in_vec[1], LP.ln1w);
+      if (l > 0) {  // centred on the mean of x2 of layer l - 1 (in LDS once all glue waves fetched it)
+        glue_fetch<GM::RPW, GM::SW, D, true, D>(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err,
+                                             sm.in_vec[1], LP.ln1w, sm.x2raw[(l - 1) & 1], &sm.in_ready[PH_FC],
+                                             (unsigned)l * NGLUE, &c0q);
         glue_input_done(sm, PH_QKV, lane);
       }
       if (leader) {
@@ -854,7 +884,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         float* vl = p.vc + (long)l * p.kv_layer;
         if (lane < rows_here) {
           const int n = row0 + lane;
-          const float v = inv_std * (row_acc<GQ>(sm, lane) - mean * sr) + cr;
+          const float v = inv_std * (row_acc<GQ>(sm, lane) - (mean - c0q) * sr) + cr;
           tstore(T + p.o_qkv + wg * GQ::SW + lane, v, tag);
           if (n >= D) {
             const int c = n < 2 * D ? n - D : n - 2 * D;
@@ -1012,18 +1042,24 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         sr = PK_G(float, LP.sf)[row0 + lane];
         cr = PK_G(float, LP.cf)[row0 + lane];
       }
-      glue_fetch<GP::RPW, GP::SW, D, true>(T + p.o_x2, D, tag, sm.x2raw, gl, p.err, sm.in_vec[1], LP.ln2w);
+      // centred on the mean of this layer's input x (in LDS once all glue
+      // waves delivered the c_attn input)
+      float c0f = 0.f;
+      glue_fetch<GP::RPW, GP::SW, D, true, D>(T + p.o_x2, D, tag, sm.x2raw[l & 1], gl, p.err, sm.in_vec[1],
+                                              LP.ln2w, sm.xraw, &sm.in_ready[PH_QKV], (unsigned)(l + 1) * NGLUE,
+                                              &c0f);
       glue_input_done(sm, PH_FC, lane);
       if (leader) {
         ++seq;
         lds_wait_ge(&sm.in_ready[PH_FC], (unsigned)(l + 1) * NGLUE, p.err);
         PK_TRACE(p, tb + 8, lane);
-        leader_ln_stats<D>(sm.x2raw, p.eps, mean, inv_std, lane);
+        leader_ln_stats<D>(sm.x2raw[l & 1], p.eps, mean, inv_std, lane);
         PK_TRACE(p, 800 + 4 * l, lane);
         lds_wait_ge(&sm.gemv_done, seq * NC, p.err);
         PK_TRACE(p, tb + 9, lane);
         if (lane < rows_here)
-          tstore(T + p.o_h + wg * GF::SW + lane, gelu_new(inv_std * (row_acc<GF>(sm, lane) - mean * sr) + cr), tag);
+          tstore(T + p.o_h + wg * GF::SW + lane,
+                 gelu_new(inv_std * (row_acc<GF>(sm, lane) - (mean - c0f) * sr) + cr), tag);
         PK_TRACE(p, tb + 10, lane);
       }
     }
@@ -1042,7 +1078,8 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         lds_wait_ge(&sm.gemv_done, ++seq * NC, p.err);
         PK_TRACE(p, tb + 12, lane);
         if (lane < rows_here)
-          tstore(T + p.o_x3 + wg * GM::SW + lane, sm.x2raw[row0 + lane] + (row_acc<GM>(sm, lane) + bias), tag);
+          tstore(T + p.o_x3 + wg * GM::SW + lane, sm.x2raw[l & 1][row0 + lane] + (row_acc<GM>(sm, lane) + bias),
+                 tag);
         PK_TRACE(p, tb + 13, lane);
       }
     }
@@ -1057,8 +1094,10 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
     sl[k] = leader && lr < rows_here ? PK_G(float, p.sl)[row0 + lr] : 0.f;
     cl[k] = leader && lr < rows_here ? PK_G(float, p.cl)[row0 + lr] : 0.f;
   }
-  glue_fetch<GM::RPW, GM::SW, D, true>(p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err,
-                                    sm.in_vec[1], p.lnfw);
+  float c0l = 0.f;
+  glue_fetch<GM::RPW, GM::SW, D, true, D>(p.tag + (long)(p.L - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err,
+                                       sm.in_vec[1], p.lnfw, sm.x2raw[(p.L - 1) & 1], &sm.in_ready[PH_FC],
+                                       (unsigned)p.L * NGLUE, &c0l);
   glue_input_done(sm, PH_LM, lane);
   if (leader) {
     ++seq;
@@ -1074,7 +1113,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
       const int lr = lane + 64 * k;
       if (lr < rows_here) {
         const int n = row0 + lr;
-        const float v = inv_std * (row_acc<GL>(sm, lr) - mean * sl[k]) + cl[k];
+        const float v = inv_std * (row_acc<GL>(sm, lr) - (mean - c0l) * sl[k]) + cl[k];
         PK_GW(float, p.logits)[n] = v;
         const u64 key = argmax_key(v, (uint32_t)n);  // -inf and NaN give 0: they never win
         best = key > best ? key : best;

@@ -159,6 +159,7 @@ struct rtg_cache {
   float* bg_part = nullptr;
   unsigned* bg_cnt = nullptr;
   float* bg_spart = nullptr;
+  float* bg_cen = nullptr;  // [2][16]: per-row centres of the folded LayerNorms' inputs
 };
 
 static void free_work(rtg_cache* c) {
@@ -388,6 +389,7 @@ static void ensure_bg_work(rtg_cache* c, const BatchedWeights* bw) {
   HIPX(hipMalloc(&c->bg_part, part * 4));
   HIPX(hipMalloc(&c->bg_cnt, groups * 4));
   HIPX(hipMalloc(&c->bg_spart, groups * 16 * 2 * 4));
+  HIPX(hipMalloc(&c->bg_cen, 2 * 16 * 4));
   HIPX(hipMemsetAsync(c->bg_cnt, 0, groups * 4, c->stream));
   HIPX(hipStreamSynchronize(c->stream));
 }
@@ -426,18 +428,32 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
   // c->att and c->h are in the GEMV input layout (xt_index, tile width tk)
   const int tk = m->wtype == W_F32 ? 16 : 32;
   const size_t NL = m->layers.size();
+  // Centres of the folded LayerNorms (two alternating per-row buffers): the
+  // GEMV input c->ln holds (x - cen_cur) * g; each LayerNorm-folded GEMV
+  // writes its rows' exact mean into the other buffer, and the residual
+  // epilogue after it centres the next input on that mean, so the fold only
+  // ever subtracts the drift of the mean between two LayerNorms.
+  float* cen_cur = c->bg_cen;
+  float* cen_next = c->bg_cen + 16;
   if (!launch_embed_stats(s, m->wte, m->wtype, m->wpe, c->token_dev, c->pos_dev, B, d, c->x, c->bg_spart,
-                          NL ? m->layers[0].ln1w : m->lnfw, c->ln))
+                          NL ? m->layers[0].ln1w : m->lnfw, c->ln, cen_cur))
     throw HipError{"embed_stats launch failed"};
   // shape of the statistics partials the last residual writer left
   int st_groups = 1, st_cols = d;
-  auto ln_in = [&](BgemvArgs& a, const float* g, const float* sv) {
+  auto ln_in = [&](BgemvArgs& a, const float* g, const float* sv, bool record) {
     a.ln_g = g; a.ln_s = sv; a.ln_part = c->bg_spart; a.ln_groups = st_groups; a.ln_cols = st_cols;
+    a.cen_in = cen_cur;
+    if (record) {
+      cen_next = cen_cur == c->bg_cen ? c->bg_cen + 16 : c->bg_cen;
+      a.cen_out = cen_next;
+    }
   };
   auto resid_out = [&](BgemvArgs& a, const BgemvPlan& pl, const float* g_next) {
     a.stats_part = c->bg_spart;
     a.xg = c->ln;
     a.g_next = g_next;
+    a.xg_cen = cen_next;
+    cen_cur = cen_next;
     st_groups = pl.groups;
     st_cols = 16 * pl.npw;
   };
@@ -448,7 +464,7 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
     {  // LN1 + c_attn; k/v of the new token into the cache
       BgemvArgs a = base();
       a.X = c->ln; a.Wt = T.qkv; a.N = 3 * d; a.K = d; a.bias = T.cq;
-      ln_in(a, L.ln1w, T.sq);
+      ln_in(a, L.ln1w, T.sq, true);
       a.epi = EPI_BIAS;
       a.qkv = BgemvQkv{c->qkv, d, d, kv, c->pos_dev};
       run(bw->pq, a);
@@ -464,7 +480,7 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
     {  // LN2 + c_fc + gelu_new
       BgemvArgs a = base();
       a.X = c->ln; a.Wt = T.fc; a.N = 4 * d; a.K = d; a.bias = T.cf;
-      ln_in(a, L.ln2w, T.sf);
+      ln_in(a, L.ln2w, T.sf, true);
       a.C = c->h; a.c_tiled = true; a.epi = EPI_BIAS_GELU;
       run(bw->pf, a);
     }
@@ -479,7 +495,7 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
   {  // ln_f + tied LM head (gpt2.rs:392-396)
     BgemvArgs a = base();
     a.X = c->ln; a.Wt = bw->lm; a.N = V; a.K = d; a.bias = bw->cl;
-    ln_in(a, m->lnfw, bw->sl);
+    ln_in(a, m->lnfw, bw->sl, false);
     a.C = c->logits; a.ldc = V; a.epi = EPI_BIAS;
     run(bw->pl, a);
   }
@@ -491,14 +507,14 @@ static void enqueue_decode_step_batched(rtg_cache* c) {
 // One decode step for all B sequences of the cache, reading the token from
 // token_dev and the position from pos_dev (both device-resident), writing the
 // argmax token back to token_dev and ids_dev[b][step]. Capturable.
-static void enqueue_decode_step(rtg_cache* c) {
+static void enqueue_decode_step(rtg_cache* c, int pos = -1) {
   const rtg_model* m = c->m;
   const int d = (int)m->cfg.n_embd, V = (int)m->cfg.vocab_size, B = (int)c->batch;
   const float eps = m->cfg.layer_norm_epsilon;
   hipStream_t s = c->stream;
   const int P = (int)m->cfg.n_positions;
   if (c->pstate) {
-    HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/false));
+    HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/false, pos));
   } else if (c->bg_part) {
     enqueue_decode_step_batched(c);
   } else {
@@ -578,7 +594,7 @@ static void forward_cached_impl(rtg_cache* c, const uint32_t* ids, size_t n, flo
     std::lock_guard<std::mutex> plock(persistent_launch_lock(m->device));
     HIPX(hipMemcpyAsync(c->token_dev, ids, 4, hipMemcpyHostToDevice, c->stream));
     set_counters(c, (int)c->len, 0);
-    HIPX(persistent_decode_step(c->pstate, c->stream, /*cooperative=*/false));
+    HIPX(persistent_decode_step(c->pstate, c->stream, /*cooperative=*/false, (int)c->len));
     if (logits_out) HIPX(hipMemcpyAsync(logits_out, c->logits, V * 4, hipMemcpyDeviceToHost, c->stream));
     HIPX(hipStreamSynchronize(c->stream));
     unsigned e = 0;
@@ -683,7 +699,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   const char* ng = getenv("RTG_NO_GRAPH");
   if (c->pstate || (ng && ng[0] == '1')) {
     for (size_t i = 1; i < steps; ++i) {
-      enqueue_decode_step(c);
+      enqueue_decode_step(c, (int)(n + i - 1));  // step i consumes the token at position n + i - 1
       sample(c->logits);
     }
   } else {
@@ -706,7 +722,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
     HIPX(hipMemcpyAsync(c->token_dev, c->ids_dev, 4, hipMemcpyDeviceToDevice, s));
     for (size_t i = 1; i < steps; ++i) {
       HIPX(hipEventRecord(evs[2 * (i - 1)], s));
-      HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/true));
+      HIPX(persistent_decode_step(c->pstate, s, /*cooperative=*/true, (int)(n + i - 1)));
       HIPX(hipEventRecord(evs[2 * (i - 1) + 1], s));
     }
     HIPX(hipStreamSynchronize(s));
@@ -1060,7 +1076,7 @@ void rtg_cache_destroy(rtg_cache* c) {
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
                   (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->logits,
-                  (void*)c->bg_part, (void*)c->bg_cnt, (void*)c->bg_spart})
+                  (void*)c->bg_part, (void*)c->bg_cnt, (void*)c->bg_spart, (void*)c->bg_cen})
     if (p) hipFree(p);
   for (auto e : c->ev)
     if (e) hipEventDestroy(e);

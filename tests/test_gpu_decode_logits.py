@@ -133,3 +133,34 @@ def test_small_generate_equals_generate_cached():
     b = m.generate_cached(prompt, 30, 0.0)
     assert a == b
     m.close()
+
+
+def test_tiled_step_logits(oracle_lib, monkeypatch):
+    """The tiled persistent step (opt-in, RTG_TILE_STEP=1 at model creation:
+    16 x 16 weight tiles per layer matrix, each LayerNorm folded on exact
+    per-block statistics): c1's 63 decode steps, and 8 steps of GPT-2 small
+    with wpe offset by 30 (|mean| / std of the residual about 1000), every
+    logits row against the oracle; ids equal the row-split step's."""
+    monkeypatch.setenv("RTG_TILE_STEP", "1")
+    sh = synth.SHAPES["small"]
+    sd = synth.make_weights(sh)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    om = oracle_lib.OracleModel.from_shape(sd, sh, threads=THREADS)
+    prompt = synth.make_tokens(32, sh.vocab_size)
+    ids = m.generate_cached(prompt, 64, 0.0)
+    worst, diffs = _steps_against_oracle(om, m, ids, 32, set(range(63)), "c1 tiled")
+    print(f"[gpu] c1 tiled step: 63 decode steps, max |d| {worst:.3e}", flush=True)
+    m.close()
+    monkeypatch.delenv("RTG_TILE_STEP")
+    ref = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    assert ref.generate_cached(prompt, 64, 0.0) == ids
+    ref.close()
+    monkeypatch.setenv("RTG_TILE_STEP", "1")
+    sd = dict(sd)
+    sd["wpe.weight"] = (sd["wpe.weight"] + np.float32(30.0)).astype(np.float32)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    om = oracle_lib.OracleModel.from_shape(sd, sh, threads=THREADS)
+    ids = m.generate_cached(prompt, 9, 0.0)
+    worst, _ = _steps_against_oracle(om, m, ids, 32, set(range(8)), "offset-30 tiled")
+    print(f"[gpu] tiled step, wpe offset 30: 8 decode steps, max |d| {worst:.3e}", flush=True)
+    m.close()

@@ -234,19 +234,29 @@ def _offset_weights(sh, offset):
     return sd
 
 
-@pytest.mark.parametrize("offset,bound", [(1.0, None), (3.0, None), (30.0, 1e-2)])
-def test_folded_layernorm_large_residual_mean(oracle_lib, offset, bound):
-    """The decode paths fold each LayerNorm into the GEMV after it:
-    LN(x) W + b = inv_std (W (x g) - mean s) + c. The subtraction cancels
-    about |mean| / std of the residual. A constant offset on wpe puts the
-    residual's mean far from zero: offset 1 gives |mean| / std of about 35 at
-    the embedding, offset 3 about 100, offset 30 about 1000. GPT-2 small (the
-    persistent kernel's width) at batch 1 (every greedy choice against the
-    oracle) and batch 4 (the batched step's logits against the oracle, within
-    the logits tolerance up to offset 3). At offset 30 the cancellation costs
-    the batched step's logits about 2e-3 (measured), beyond the tolerance:
-    that case asserts the measured bound instead, so that any growth shows."""
+@pytest.mark.parametrize("offset", [1.0, 3.0, 30.0])
+def test_folded_layernorm_large_residual_mean(oracle_lib, offset):
+    """The decode paths fold each LayerNorm into the GEMV after it. Folded
+    naively, LN(x) W + b = inv_std (W (x g) - mean s) + c cancels about
+    |mean| / std of the residual; both paths therefore centre the GEMV input
+    first: the persistent step on the mean of each glue wave's share of the
+    inputs (the fold adds sum_w (mu_w - mean) s_w), the batched step on the
+    previous LayerNorm's row mean (the fold subtracts only the drift). A
+    constant offset on wpe puts the residual's mean far from zero: offset 1
+    gives |mean| / std of about 35 at the embedding, offset 3 about 100,
+    offset 30 about 1000. GPT-2 small at batch 1 (every greedy choice
+    against the oracle, and the persistent step's logits of 8 decode steps)
+    and batch 4 (the batched step's logits of 4 steps).
+
+    Bar: within 1e-3 + 1e-4 |ref| of the oracle at offsets 1 and 3. At offset
+    30 the reference's own f32 arithmetic is the limit: its LayerNorm sums
+    768 values of ~30 one after another in f32, and its logits differ from
+    exact (float64, tests/ref64.py) arithmetic by up to 2.3e-3 on these rows,
+    while both decode paths stay within ~1.5e-4 of float64. There each path
+    is held to the bar against float64 and, against the oracle, to the bar
+    widened by the oracle's own distance from float64 on that row."""
     O = oracle_lib
+    from tests import ref64
     sh = synth.SHAPES["small"]
     sd = _offset_weights(sh, offset)
     x0 = sd["wte.weight"][:64] + sd["wpe.weight"][:64]
@@ -254,28 +264,52 @@ def test_folded_layernorm_large_residual_mean(oracle_lib, offset, bound):
     print(f"[gpu] offset {offset}: |mean|/std of the embedding rows >= {ratio:.1f}", flush=True)
     m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
     om = O.OracleModel.from_shape(sd, sh, threads=THREADS)
+    exact = offset >= 30.0
+
+    def check(got, ref, seq, what):
+        """got/ref: one logits row of the last token of seq."""
+        if not exact:
+            return assert_logits_close(got, ref, what)
+        f64 = ref64.forward(sd, seq, sh.n_layer, sh.n_head)[-1]
+        d = assert_logits_close(got, f64, f"{what} against float64")
+        oracle_err = float(np.max(np.abs(np.asarray(ref, np.float64) - f64)))
+        excess = float(np.max(np.abs(np.asarray(got, np.float64) - ref) - (ATOL + RTOL * np.abs(ref)) - oracle_err))
+        assert excess <= 0, f"{what}: against the oracle beyond the bar plus the oracle's own error {oracle_err:.3e}"
+        return d
+
     prompt = synth.make_tokens(32, sh.vocab_size, stream=740)
     ids = m.generate_cached(prompt, 48, 0.0)
     check_greedy_along(om, prompt, ids, f"persistent step, wpe offset {offset}")
+    # the persistent step's logits (forward_cached with one token at batch 1)
+    c, oc = m.new_cache(), om.new_cache()
+    m.forward_cached(prompt, c)
+    om.forward_cached(prompt, oc)
+    worst1 = 0.0
+    steps = 4 if exact else 8
+    for t in range(steps):
+        tok = [int(ids[32 + t])]
+        seq = [int(v) for v in ids[:33 + t]]
+        worst1 = max(worst1, check(m.forward_cached(tok, c)[0], om.forward_cached(tok, oc)[0], seq,
+                                   f"offset {offset} persistent step {t}"))
+    c.close()
     B = 4
     prompts = np.stack([synth.make_tokens(16, sh.vocab_size, stream=750 + b) for b in range(B)])
     c = m.new_cache(batch=B)
-    lg = m.forward_cached_batched(prompts, c)
+    m.forward_cached_batched(prompts, c)
     ocs = [om.new_cache() for _ in range(B)]
+    seqs = [list(map(int, prompts[b])) for b in range(B)]
     nxt = np.array([[O.argmax(om.forward_cached(prompts[b], ocs[b])[-1])] for b in range(B)], dtype=np.uint32)
     worst = 0.0
-    for t in range(4):
+    for t in range(2 if exact else 4):
         lg = m.forward_cached_batched(nxt, c)
         new = []
         for b in range(B):
+            seqs[b].append(int(nxt[b, 0]))
             ref = om.forward_cached([int(nxt[b, 0])], ocs[b])
-            if bound is None:
-                worst = max(worst, assert_logits_close(lg[b], ref, f"offset {offset} step {t} seq {b}"))
-            else:
-                worst = max(worst, float(np.max(np.abs(lg[b].astype(np.float64) - ref))))
+            worst = max(worst, check(lg[b, 0], ref[0], seqs[b], f"offset {offset} batched step {t} seq {b}"))
             new.append([O.argmax(ref[0])])
         nxt = np.array(new, dtype=np.uint32)
-    print(f"[gpu] offset {offset}: batched step logits max |d| {worst:.3e}", flush=True)
-    if bound is not None:
-        assert worst <= bound, f"offset {offset}: batched step logits max |d| {worst:.3e}"
+    vs = "float64" if exact else "the oracle"
+    print(f"[gpu] offset {offset}: max |d| against {vs}: persistent step {worst1:.3e}, batched step {worst:.3e}",
+          flush=True)
     m.close()
