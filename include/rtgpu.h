@@ -34,7 +34,22 @@ typedef struct {
   char* error_msg; /* NULL on success; free with rtg_free_error_message */
 } rtg_result;
 
-/* Gpt2Config, gpt2.rs:82-104. */
+/* Gpt2Config, gpt2.rs:82-104. The fields are public in the reference, which
+ * takes head_dim = n_embd / n_head (gpt2.rs:349-352). This build accepts the
+ * configurations its kernels are written for and refuses the others when the
+ * model is created, before anything is uploaded, with these errors:
+ *   "n_embd <d> is not divisible by n_head <h>"   (the reference would
+ *       truncate head_dim and read past its rows)
+ *   "head_dim <hd> > 64 is not supported"         (head_dim <= 64 only)
+ *   "n_embd <d> must be a multiple of 8"          (16-byte row vectors)
+ * Every GPT-2 checkpoint (head_dim 64, n_embd 768 / 1024 / 1280 / 1600) and
+ * the reference's own test configuration (n_embd 8, 2 heads) are accepted.
+ * The fastest batch-1 decode step (one persistent kernel per token) is built
+ * for (n_embd, vocab_size) = (128, 512), (768, 50257), (1024, 50257) in f32
+ * and bf16 storage, (1280, 50257) in f32 and (1600, 50257) in bf16; other
+ * accepted shapes decode through the batched step's kernel graph at batch 1
+ * (same results within the logits tolerance, about 4.5 us per kernel launch,
+ * 5 launches per layer). */
 typedef struct {
   size_t vocab_size;
   size_t n_positions;
@@ -159,7 +174,9 @@ rtg_result rtg_generate(const rtg_model* model, const uint32_t* prompt, size_t n
 rtg_result rtg_generate_cached(const rtg_model* model, const uint32_t* prompt, size_t n, size_t max_new,
                                float temperature, uint64_t seed, uint32_t* out);
 /* Gpt2Model::generate_with_config, gpt2.rs:447-474 (+ sample_logits :871-906).
- * out receives n + max(1, cfg->max_new_tokens) ids. */
+ * out receives n + max(1, cfg->max_new_tokens) ids. Non-greedy token choice
+ * runs on the device for vocab_size <= 65536 (every GPT-2 vocabulary);
+ * beyond it the call returns "vocabulary too large for the device sampler". */
 rtg_result rtg_generate_with_config(const rtg_model* model, const uint32_t* prompt, size_t n,
                                     const rtg_gen_config* cfg, uint32_t* out);
 

@@ -243,7 +243,6 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
   // the input rows' LayerNorm statistics partials, loaded now and merged in
   // the epilogue (the kernel that wrote x left them)
   float2 lnp[LNG_PER];
-  float cen_in = 0.f, xg_cen = 0.f;  // the rows' LayerNorm centres, loaded now too
   if (nt > 0) {
 #pragma unroll
     for (int d = 0; d < DEPTH_; ++d) issue(d, d);
@@ -255,9 +254,7 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
       const int gg = min(sub + 16 * i, a.ln_groups - 1);
       lnp[i] = *reinterpret_cast<const float2*>(a.ln_part + ((size_t)gg * 16 + mrow) * 2);
     }
-    if (a.cen_in) cen_in = a.cen_in[mrow];
   }
-  if (a.xg_cen) xg_cen = a.xg_cen[min((tid & 255) >> 4, a.M - 1)];
   const int m = tid >> 4;
   const bool early = a.epi == EPI_BIAS_RESID && !a.qkv.q;
   EpiIn eo[NPW];
@@ -348,10 +345,10 @@ __device__ __forceinline__ void bgemv_unit(const BgemvArgs& a, int g, int s, flo
   if constexpr (LNG) {
     row_stats_merge(a, lnp, mean, inv_std);
     // the input was centred on cen_in[m]: only the drift of the mean remains
-    mc = mean - cen_in;
+    mc = mean - (a.cen_in && m < a.M ? a.cen_in[m] : 0.f);
     if (a.cen_out && g == 0 && (tid & 15) == 0 && m < a.M) a.cen_out[m] = mean;
   }
-  const float xc = xg_cen;
+  const float xc = a.xg_cen && m < a.M ? a.xg_cen[m] : 0.f;
   if (!early) {
 #pragma unroll
     for (int j = 0; j < NPW; ++j) eo[j] = load_epi(a, m, (g * NPW + j) * 16 + (tid & 15), LNG);
