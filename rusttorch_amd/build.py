@@ -26,7 +26,7 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", f"-I{os
 SOURCES = ["kernels.hip", "decode_persistent.hip", "decode_persistent_inst_mini.hip",
            "decode_persistent_inst_small.hip", "decode_persistent_inst_medium.hip",
            "decode_persistent_inst_large.hip", "rtg_runtime.cpp", "safetensors_reader.cpp",
-           "tokenizer.cpp", "sampling.hip", "bgemv.hip", "scratch.hip", "decode_tile.hip"]
+           "tokenizer.cpp", "sampling.hip", "bgemv.hip", "scratch.hip", "decode_tile.hip", "rows.hip"]
 
 
 def _compile(src: str) -> str:

@@ -21,6 +21,7 @@
 #include "decode_persistent.h"
 #include "bgemv.h"
 #include "kernels.h"
+#include "rows.h"
 #include "safetensors_reader.h"
 #include "scratch.h"
 
@@ -115,6 +116,7 @@ struct rtg_model {
   std::vector<LayerW> layers;
   size_t nparams = 0;
   PersistentPlan* pplan = nullptr;
+  RowsPlan* rplan = nullptr;  // multi-row forward (short prompts), null where unsupported
   std::mutex bw_mu;
   std::unique_ptr<BatchedWeights> bw;
   // Pool of caches reused by the generate entry points (keyed by batch).
@@ -154,6 +156,7 @@ struct rtg_cache {
   hipGraphExec_t graph_exec = nullptr;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   PersistentState* pstate = nullptr;
+  RowsState* rstate = nullptr;  // the multi-row forward's flags and work rows
   // batched decode step (bgemv): split-k partials and counters, per-group
   // LayerNorm statistics partials of the residual stream
   float* bg_part = nullptr;
@@ -247,6 +250,7 @@ rtg_model::~rtg_model() {
   for (auto& kv : pool) rtg_cache_destroy(kv.second);
   pool.clear();
   if (pplan) persistent_plan_destroy(pplan);
+  if (rplan) rows_plan_destroy(rplan);
   if (arena) hipFree(arena);
 }
 
@@ -544,6 +548,43 @@ static void set_counters(rtg_cache* c, int pos, int step) {
   HIPX(hipMemcpyAsync(c->step_dev, &hv[1], 4, hipMemcpyHostToDevice, c->stream));
 }
 
+// The multi-row forward runs S sequences x T tokens of a cache of batch S in
+// one launch (RTG_NO_ROWS=1: the per-op prefill kernels instead).
+static bool rows_path(const rtg_cache* c, size_t S, size_t T) {
+  const char* off = getenv("RTG_NO_ROWS");
+  if (off && off[0] == '1') return false;
+  return c->m->rplan && S == c->batch && rows_supported(c->m->rplan, (int)S, (int)T);
+}
+
+// Enqueues the multi-row forward on the cache's stream (the caller holds
+// persistent_launch_lock until the stream drains): ids_dev [S*T] at position
+// past, logits [S*T][V]; state st (default: the cache's own, made on first use).
+static void enqueue_rows(rtg_cache* c, const uint32_t* ids_dev, size_t S, size_t T, size_t past, float* logits,
+                         RowsState* st = nullptr) {
+  const rtg_model* m = c->m;
+  if (!st) {
+    if (!c->rstate) {
+      c->rstate = rows_state_create(m->rplan);
+      if (!c->rstate) throw HipError{"multi-row forward: state allocation failed"};
+    }
+    st = c->rstate;
+  }
+  HIPX(rows_forward(m->rplan, st, c->stream, c->k, c->v, (long)c->layer_stride, ids_dev, (int)S, (int)T, (int)past,
+                    nullptr, logits));
+}
+
+// After the stream has drained: a bounded wait of the multi-row forward that
+// timed out becomes an error (its word is cleared for the next launch).
+static void check_rows(RowsState* st) {
+  rows_dump_trace();
+  unsigned e = 0;
+  HIPX(hipMemcpy(&e, rows_err(st), 4, hipMemcpyDeviceToHost));
+  if (e) {
+    HIPX(hipMemset(rows_err(st), 0, 4));
+    throw HipError{fmt("multi-row forward timed out waiting for a peer (phase %u)", e)};
+  }
+}
+
 static void ensure_graph(rtg_cache* c) {
   if (c->graph_exec) return;
   HIPX(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
@@ -614,6 +655,15 @@ static void forward_cached_impl(rtg_cache* c, const uint32_t* ids, size_t n, flo
     HIPX(hipMemcpyAsync(c->token_dev, ids, B * 4, hipMemcpyHostToDevice, c->stream));
     set_counters(c, (int)c->len, 0);
     enqueue_decode_step(c);
+  } else if (rows_path(c, B, n)) {
+    std::lock_guard<std::mutex> plock(persistent_launch_lock(m->device));
+    HIPX(hipMemcpyAsync(c->ids_in, ids, B * n * 4, hipMemcpyHostToDevice, c->stream));
+    enqueue_rows(c, c->ids_in, B, n, c->len, c->logits);
+    if (logits_out) HIPX(hipMemcpyAsync(logits_out, c->logits, B * n * V * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPX(hipStreamSynchronize(c->stream));
+    check_rows(c->rstate);
+    c->len += n;
+    return;
   } else {
     HIPX(hipMemcpyAsync(c->ids_in, ids, B * n * 4, hipMemcpyHostToDevice, c->stream));
     enqueue_prefill(c, cache_work(c), c->ids_in, B, n, c->len, 0);
@@ -679,11 +729,13 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   // The persistent step's workgroups wait on each other: no second persistent
   // step of this process may be in flight on the device (another thread's
   // cache) until this stream has drained.
+  const bool rows = rows_path(c, B, n);
   std::unique_lock<std::mutex> plock;
-  if (c->pstate) plock = std::unique_lock<std::mutex>(persistent_launch_lock(m->device));
+  if (c->pstate || rows) plock = std::unique_lock<std::mutex>(persistent_launch_lock(m->device));
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
   HIPX(hipEventRecord(c->ev[0], s));
-  enqueue_prefill(c, cache_work(c), c->ids_in, B, n, 0, 0);
+  if (rows) enqueue_rows(c, c->ids_in, B, n, 0, c->logits);
+  else enqueue_prefill(c, cache_work(c), c->ids_in, B, n, 0, 0);
   // argmax of the last row of each sequence (extract_row(logits, n-1))
   launch_argmax(s, c->logits + (n - 1) * V, (long)(n * V), (int)B, (int)V, c->keys);
   // finalize advances pos by one: after it, pos = n, the position of the
@@ -737,6 +789,7 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   std::vector<uint32_t> gen(B * P);
   HIPX(hipMemcpyAsync(gen.data(), c->ids_dev, B * P * 4, hipMemcpyDeviceToHost, s));
   HIPX(hipStreamSynchronize(s));
+  if (rows) check_rows(c->rstate);
   if (c->pstate) {
     persistent_dump_trace(c->pstate);
     unsigned e = 0;
@@ -959,6 +1012,10 @@ rtg_result build_model(const rtg_config* cfg, Lookup& lk, rtg_storage storage, r
       pw.layers.push_back({l.wqkv, l.waproj, l.wfc, l.wmproj, l.bqkv, l.baproj, l.bfc, l.bmproj, l.ln1w, l.ln1b,
                            l.ln2w, l.ln2b});
     m->pplan = persistent_plan_create(pw);
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      m->rplan = rows_plan_create(pw, cus);
   }
   *out = m.release();
   return ok();
@@ -1073,6 +1130,7 @@ void rtg_cache_destroy(rtg_cache* c) {
   if (c->stream) hipStreamSynchronize(c->stream);
   destroy_graph(c);
   if (c->pstate) persistent_state_destroy(c->pstate);
+  if (c->rstate) rows_state_destroy(c->rstate);
   free_work(c);
   for (void* p : {(void*)c->k, (void*)c->v, (void*)c->pos_dev, (void*)c->step_dev, (void*)c->keys,
                   (void*)c->token_dev, (void*)c->ids_dev, (void*)c->ids_in, (void*)c->logits,
@@ -1121,6 +1179,41 @@ rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const ui
   return rtg_forward_cached_batched(model, cache, ids, n, logits_out);
 }
 
+// rtg_forward_cached_noalloc for a prompt the multi-row forward takes: its
+// state in the scratch array (the 64 KiB head, then its work rows), the
+// logits after it; the same kernel and inputs as rtg_forward_cached's.
+static rtg_result noalloc_rows(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
+                               float* logits_out) {
+  const size_t V = model->cfg.vocab_size;
+  const size_t state = align_up(rows_state_bytes(model->rplan, false), 256) / 4;
+  if (state + n * V > kScratchHeadFloats + kScratchFloats)
+    return err(fmt("rtg_forward_cached_noalloc: %zu new tokens need %zu bytes of scratch; it holds %zu", n,
+                   (state + n * V - kScratchHeadFloats) * 4, kScratchFloats * 4));
+  try {
+    hipError_t he = hipSuccess;
+    float* sp = scratch_device_ptr(model->device, &he);
+    HIPX(he);
+    static_assert(rows_state_head_bytes() == kScratchHeadFloats * sizeof(float), "scratch head");
+    std::lock_guard<std::mutex> slock(scratch_lock(model->device));
+    std::lock_guard<std::mutex> plock(persistent_launch_lock(model->device));
+    RowsState st;  // over the scratch array (one region per buffer): nothing is allocated
+    st.mem = sp;
+    st.fresh = false;
+    float* logits = sp + state;
+    HIPX(hipMemcpyAsync(cache->ids_in, ids, n * 4, hipMemcpyHostToDevice, cache->stream));
+    enqueue_rows(cache, cache->ids_in, 1, n, cache->len, logits, &st);
+    if (logits_out) HIPX(hipMemcpyAsync(logits_out, logits, n * V * 4, hipMemcpyDeviceToHost, cache->stream));
+    HIPX(hipStreamSynchronize(cache->stream));
+    check_rows(&st);
+    cache->len += n;
+  } catch (const HipError& he) {
+    return err(he.msg);
+  } catch (const std::exception& ex) {
+    return err_internal(ex);
+  }
+  return ok();
+}
+
 rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
                                       float* logits_out) {
   if (!model || !cache || (n && !ids)) return err("null argument");
@@ -1150,10 +1243,12 @@ rtg_result rtg_forward_cached_noalloc(const rtg_model* model, rtg_cache* cache, 
   // GEMMs run unsplit (the same sums in another order), so the limit is
   // exactly the activations' size and grows monotonically with n
   if (need + pw > kScratchFloats) pw = 0;
+  if (rows_path(cache, 1, n)) return noalloc_rows(model, cache, ids, n, logits_out);
   try {
     hipError_t he = hipSuccess;
     float* sp = scratch_device_ptr(model->device, &he);
     HIPX(he);
+    sp += kScratchHeadFloats;
     // every call on this device shares the array: one pass at a time (the
     // call has drained its stream when it returns)
     std::lock_guard<std::mutex> slock(scratch_lock(model->device));

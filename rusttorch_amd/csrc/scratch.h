@@ -14,10 +14,16 @@ namespace rtg {
 // prefill GEMMs' split-k partials use what is left, else the GEMMs run
 // unsplit.
 constexpr size_t kScratchFloats = (size_t)4 << 20;
+// The array also holds, ahead of those 16 MiB, 64 KiB that only the multi-row
+// forward (short prompts, rows.h) uses: its flag words, epoch and counters,
+// which must keep what its previous launch on this device left (zeros before
+// the first). Its work rows and logits then take the 16 MiB that follow.
+constexpr size_t kScratchHeadFloats = (size_t)16 << 10;
 
 // Device address of `device`'s copy of the array (looked up once per device
-// with hipGetSymbolAddress, with that device current; the current device is
-// restored afterwards). Null with *err set on failure.
+// with hipGetSymbolAddress, with that device current, which also clears the
+// 64 KiB head; the current device is restored afterwards). Null with *err set
+// on failure. The 16 MiB of activations start kScratchHeadFloats after it.
 float* scratch_device_ptr(int device, hipError_t* err);
 
 // Held by a call from its first use of `device`'s array until its stream has

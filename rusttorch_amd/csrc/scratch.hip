@@ -11,7 +11,7 @@
 
 namespace rtg {
 
-static __device__ __align__(256) float scratch[kScratchFloats];
+static __device__ __align__(256) float scratch[kScratchHeadFloats + kScratchFloats];
 
 float* scratch_device_ptr(int device, hipError_t* err) {
   constexpr int kMaxDevices = 64;
@@ -28,6 +28,7 @@ float* scratch_device_ptr(int device, hipError_t* err) {
     if (e == hipSuccess && cur != device) e = hipSetDevice(device);
     void* p = nullptr;
     if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipMemset(p, 0, kScratchHeadFloats * sizeof(float));
     if (cur != device) {
       const hipError_t r = hipSetDevice(cur);
       if (e == hipSuccess) e = r;
