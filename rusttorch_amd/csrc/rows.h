@@ -44,9 +44,21 @@ unsigned* rows_err(RowsState* s);
 // sequence's first new token at position past, or *pos_dev when pos_dev is
 // set; logits [S*T][V]. The caller must hold persistent_launch_lock(device)
 // from the launch until the stream has drained.
+// With fin set, the launch also finishes a greedy step the way launch_argmax
+// + launch_finalize do: keys [S] (zero on entry, cleared again), the argmax
+// token of each sequence's last row into token [S] and ids_out[s * ld_ids +
+// *step], then *pos and *step advanced by one.
+struct RowsFinish {
+  unsigned long long* keys;
+  uint32_t* token;
+  uint32_t* ids_out;
+  int ld_ids;
+  int* pos;
+  int* step;
+};
 hipError_t rows_forward(const RowsPlan* p, RowsState* s, hipStream_t stream, float* kc, float* vc, long kv_layer,
                         const uint32_t* ids_dev, int S, int T, int past, const int* pos_dev, float* logits,
-                        uint64_t* trace = nullptr);
+                        const RowsFinish* fin = nullptr, uint64_t* trace = nullptr);
 // With $RTG_ROWS_TRACE set, every launch records per-workgroup phase
 // timestamps (100 MHz clock; [256][512] u64: word 2 (8 (l + 1) + phase) + k,
 // k = 0 inputs ready, 1 outputs published; the LM head is layer L, phase 0;

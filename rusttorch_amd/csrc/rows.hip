@@ -158,7 +158,7 @@ rk::u64* trace_buf() {
 
 hipError_t rows_forward(const RowsPlan* p, RowsState* s, hipStream_t stream, float* kc, float* vc, long kv_layer,
                         const uint32_t* ids_dev, int S, int T, int past, const int* pos_dev, float* logits,
-                        uint64_t* trace) {
+                        const RowsFinish* fin, uint64_t* trace) {
   if (!rows_supported(p, S, T)) return hipErrorInvalidValue;
   rk::RParams a = p->base;
   a.kc = kc;
@@ -182,6 +182,14 @@ hipError_t rows_forward(const RowsPlan* p, RowsState* s, hipStream_t stream, flo
   a.p0_stride = s->fresh ? (long)(p->p0q + p->p0f) : 0;
   a.p0_fc = s->fresh ? (long)p->p0q : 0;
   a.logits = logits;
+  if (fin) {
+    a.keys = fin->keys;
+    a.token = fin->token;
+    a.ids_out = fin->ids_out;
+    a.ld_ids = fin->ld_ids;
+    a.fin_pos = fin->pos;
+    a.step = fin->step;
+  }
   a.flags = head_flags(s->mem);
   a.epoch = head_epoch(s->mem);
   a.done = head_done(s->mem);

@@ -16,8 +16,8 @@
 //   PROJ   (attn c_proj on O)          -> partials P1
 //   ROW2   one workgroup per row: x += P1 sums + bias; LN2(x) -> XN
 //   FC     (c_fc on XN)                -> partials P0
-//   MLP    (mlp c_proj on gelu_new(P0 sums + bias), formed by its A loader)
-//                                      -> partials P1
+//   MLP    (mlp c_proj on gelu_new(P0 sums + bias), formed as its operand
+//          is read)                    -> partials P1
 //   ROW3   x += P1 sums + bias; LN1 of the next layer (ln_f after the last)
 //          -> XN
 //   LM     tied LM head, every workgroup a strided set of 32-column tiles.
@@ -43,7 +43,11 @@
 // stale cached copy (caches are invalidated between launches) and the readers
 // on one XCD share its L2. Device-scope loads of one shared region each (the
 // mode of a caller-provided workspace too small for the layered regions)
-// were measured 3-13 us per phase at 72-256 readers. The MLP partials P1
+// were measured 3-13 us per phase at 72-256 readers. Weight slices and (up to
+// d = 768) the activation rows of a GEMM tile arrive by DMA into LDS as whole
+// row runs (a lane-per-row load touches 64 lines per instruction: the MLP
+// projection's input took 4.6 us that way); the MLP projection's weights,
+// prefetched a phase ahead, come into registers. The MLP partials P1
 // have one reader per row and are always read with device-scope loads from
 // one region; every reuse of a region is ordered behind all of its readers
 // through the flag graph (each reader is an ancestor of the next writer).
@@ -51,6 +55,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "argmax_key.h"
 #include "attn_core.h"
 #include "gelu.h"
 
@@ -75,6 +80,8 @@ constexpr int KWMAX = 64;           // k values per lane of a layer tile
 constexpr int TRACE_WORDS = 1024;   // per workgroup: 4 per (layer, phase), t0 last
 constexpr unsigned SPIN_CAP = 1u << 20;
 
+// Phases of a layer in program order: a workgroup's flag only ever grows, so
+// a flag at or past a phase's number means that phase's work is published.
 enum { PH_QKV = 0, PH_ATT = 1, PH_PROJ = 2, PH_ROW2 = 3, PH_FC = 4, PH_MLP = 5, PH_ROW3 = 6 };
 // Sequence number of phase ph of layer l; the embedding is PH_ROW3 of layer -1.
 __host__ __device__ constexpr unsigned seq_of(int l, int ph) { return (unsigned)((l + 1) * 8 + ph); }
@@ -130,6 +137,17 @@ struct RParams {
   long p0_fc;                  //   [KSF][MR][4D] at this offset
   float* p1;                   // attn / mlp c_proj partials [ks][MR][D]
   float* logits;       // [M][V]
+  // Optional greedy finish (keys set): the argmax of each sequence's last row
+  // (argmax_key, gpt2.rs:858-868) into keys[s]; the last workgroup to finish
+  // then writes token[s] = that index and ids_out[s * ld_ids + *step], clears
+  // the keys and advances *fin_pos and *step by one (the finalize of the
+  // reference's generate loop, gpt2.rs:431-437).
+  unsigned long long* keys;
+  uint32_t* token;
+  uint32_t* ids_out;
+  int ld_ids;
+  int* fin_pos;
+  int* step;
   u64* flags;          // [G][FS]
   u64* epoch;
   unsigned* done;
@@ -165,6 +183,11 @@ template <bool FRESH>
 __device__ __forceinline__ float4 ldx4(const float* p) {
   if constexpr (FRESH) return ld4(p);
   else return ldc4(p);
+}
+template <bool FRESH>
+__device__ __forceinline__ float ldx1(const float* p) {
+  if constexpr (FRESH) return *RK_G(float, p);
+  else return __hip_atomic_load(RK_GW(float, const_cast<float*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void stc(float* p, float v) {
   __hip_atomic_store(RK_GW(float, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -206,14 +229,21 @@ __device__ __forceinline__ void wait_for(const RParams& p, int n, F prod, u64 ta
     const int lane = threadIdx.x & 63;
     unsigned spins = 0;
     while (true) {
+      // all of a lane's flags in flight at once (no short-circuit between them)
+      // (branch-free: lanes past n re-read producer n - 1), as many rounds
+      // of 64 as n needs
+      u64 f[4];
+      const int nr = (n + 63) >> 6;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k < nr) f[k] = ld_flag(p.flags + (size_t)prod(min(lane + 64 * k, n - 1)) * FS);
+      const bool failed = err_set(p);  // in the same round trip as the flags
       bool ok = true;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = lane + 64 * k;
-        if (i < n) ok = ok && ld_flag(p.flags + (size_t)prod(i) * FS) >= target;
-      }
+      for (int k = 0; k < 4; ++k)
+        if (k < nr) ok &= f[k] >= target;
       if (__all(ok)) break;
-      if (++spins > SPIN_CAP || err_set(p)) {
+      if (++spins > SPIN_CAP || failed) {
         if (lane == 0 && spins > SPIN_CAP)
           __hip_atomic_store(RK_GW(unsigned, p.err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
@@ -244,10 +274,18 @@ __device__ __forceinline__ void signal(const RParams& p, u64 val) {
 // at dst, lane i at dst + 16 i), streaming (nt). The loads count in vmcnt but
 // occupy no registers; the compiler does not see them, so the wave waits for
 // them itself (lds_dma_wait) before reading dst.
+// POL: 0 streaming (nt: weights, read once), 1 cached (data in a region of
+// its own), 2 device scope (data in a shared region).
+template <int POL = 0>
 __device__ __forceinline__ void lds_dma16(const float* src, float* dst) {
   const unsigned m0v =
       __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(const __attribute__((address_space(3))) float*)dst);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0v) : "memory", "m0");
+  if constexpr (POL == 0)
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0v) : "memory", "m0");
+  else if constexpr (POL == 1)
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v) : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(src), "s"(m0v) : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -282,14 +320,30 @@ __device__ __forceinline__ int swz(int row) {
 // k [kw0, kw0 + 2 KW), into its LDS region wl (KW / 4 KiB): instruction t
 // loads slots 64 t .. 64 t + 63, so each row's k range arrives as whole
 // contiguous runs (in a permuted lane order).
-template <int KW>
+template <int KW, int POL = 0>
 __device__ __forceinline__ void w_dma(float* wl, const float* W, int K, int N, int n0, int kw0, int lane) {
   constexpr int CPR = KW / 2;
 #pragma unroll
   for (int t = 0; t < KW / 4; ++t) {
     const int sl = 64 * t + lane, row = sl / CPR, c = (sl % CPR) ^ swz<CPR>(row);
-    lds_dma16(W + (size_t)min(n0 + row, N - 1) * K + kw0 + 4 * c, wl + 256 * t);
+    lds_dma16<POL>(W + (size_t)min(n0 + row, N - 1) * K + kw0 + 4 * c, wl + 256 * t);
   }
+}
+// The same for an activation slice: rows 0.. 31 of X (row stride ldx; rows
+// past M re-read row M - 1: they only feed output rows that are never stored).
+template <int KW, bool FRESH>
+__device__ __forceinline__ void a_dma(float* al, const float* X, int ldx, int M, int kw0, int lane) {
+  w_dma<KW, FRESH ? 1 : 2>(al, X, ldx, M, 0, kw0, lane);
+}
+// Every wave's vector memory instructions except its last n have completed,
+// then the workgroup barrier; one lane publishes the flag.
+template <int N>
+__device__ __forceinline__ void signal_keep(const RParams& p, u64 val) {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_store(RK_GW(u64, p.flags + (size_t)blockIdx.x * FS), val, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int KW, bool FRESH>
@@ -305,7 +359,8 @@ __device__ __forceinline__ void a_rows(float4 (&a)[KW / 4], const float* X, int 
   }
 }
 
-// MLP projection input: gelu_new(c_fc partials summed in k order + bias).
+// MLP projection input in registers: gelu_new(c_fc partials summed in k
+// order + bias), lane-per-row loads.
 template <int KW, int KS, bool FRESH>
 __device__ __forceinline__ void a_gelu(float4 (&a)[KW / 4], const float* P, int N, int M, const float* bias, int kl,
                                        int lane) {
@@ -330,6 +385,16 @@ __device__ __forceinline__ void a_gelu(float4 (&a)[KW / 4], const float* P, int 
   }
 }
 
+// The wave's W values of a tile in registers, lane (h, i) = W[n0 + i][kl + 4j
+// .. +4) (cached loads: the lines of 64 rows per instruction are re-read by
+// the next ones from L2).
+template <int KW>
+__device__ __forceinline__ void w_regs(float4 (&w)[KW / 4], const float* W, int K, int N, int n0, int kl, int lane) {
+  const float* src = W + (size_t)min(n0 + (lane & 31), N - 1) * K + kl;
+#pragma unroll
+  for (int j = 0; j < KW / 4; ++j) w[j] = ld4(src + 4 * j);
+}
+
 __device__ __forceinline__ void mma4(const float4& a, const float4& w, floatx16& c0, floatx16& c1) {
   c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, w.x, c0, 0, 0, 0);
   c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, w.y, c1, 0, 0, 0);
@@ -343,6 +408,18 @@ __device__ __forceinline__ float4 w_chunk(const float* wl, int q, int lane) {
   constexpr int CPR = KW / 2;
   const int i = lane & 31, c = (lane >> 5) * (KW / 4) + q;
   return *reinterpret_cast<const float4*>(wl + 4 * (i * CPR + (c ^ swz<CPR>(i))));
+}
+
+// A and W from the wave's LDS regions (w_dma's layout).
+template <int KW>
+__device__ __forceinline__ floatx16 mma_lds(const float* al, const float* wl, int lane) {
+  lds_dma_wait();
+  floatx16 c0, c1;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) c0[e] = c1[e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < KW / 4; ++j) mma4(w_chunk<KW>(al, j, lane), w_chunk<KW>(wl, j, lane), c0, c1);
+  return c0 + c1;
 }
 
 // A in registers, W from the wave's LDS region (w_dma's layout).
@@ -601,19 +678,29 @@ __device__ __forceinline__ void att_gather(const RParams& p, AttLds& A, const fl
 template <int D>
 struct RSmem {
   using C = RCfg<D>;
-  // per-wave weight regions (w_dma layout): c_attn + attn c_proj tiles in the
-  // first half of a layer (the attention items' LDS after them), c_fc + mlp
-  // c_proj tiles in the second
+  // activation slices through LDS as well where it has room for them
+  static constexpr bool ADMA = D <= 768;
+  // per-wave slices (w_dma layout): the c_attn and attn c_proj weights in the
+  // first half of a layer (c_attn's activations where the attention items'
+  // LDS goes later; attn c_proj's where the c_attn weights were), the c_fc
+  // weights and activations in the second, replaced by mlp c_proj's once c_fc
+  // is computed
   static constexpr int WQ = NCW * C::KWQ * 64, WP = NCW * C::KWP * 64;
   static constexpr int WF = NCW * C::KWF * 64, WM = NCW * C::KWM * 64;
+  // the second half: c_fc's weights and activations, then the KSF c_fc
+  // partial slices of the mlp c_proj's input
+  static constexpr int H2A = 2 * WF, H2B = C::KSF * WM + NCW * 256;  // + each wave's c_fc bias slice
+  static constexpr int H2 = ADMA ? (H2A > H2B ? H2A : H2B) : WF;
   struct Half1 {
     float wq[WQ];
     float wp[WP];
-    AttLds att;
+    union {
+      AttLds att;
+      float aq[ADMA ? WQ : 1];
+    };
   };
   struct Half2 {
-    float wf[WF];
-    float wm[WM];
+    float x[H2];
   };
   float red[NCW * 16 * 64];  // the compute waves' 32x32 tiles
   u64 trs[TRACE_WORDS];
@@ -633,6 +720,8 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
   constexpr int H = C::H, NU = C::NU;
   __shared__ RSmem<D> sm;
   static_assert(sizeof(RSmem<D>) <= 160 * 1024, "LDS");
+  constexpr bool ADMA = RSmem<D>::ADMA;
+  static_assert(!ADMA || C::KWP <= C::KWQ, "attn c_proj activations in the c_attn weight region");
   float* red = sm.red;
   AttLds& att = sm.h1.att;
   u64* trs = sm.trs;
@@ -698,24 +787,33 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
     // weights of this layer's c_attn and attn c_proj tiles, in flight into LDS from here
     float* wq = sm.h1.wq + wave * C::KWQ * 64;
     float* wp = sm.h1.wp + wave * C::KWP * 64;
+    // k range of this compute wave in its tile (kw0: both halves) and of this lane (kl)
     const int cq = wg / C::KSQ, zq = wg % C::KSQ;
-    const int klq = zq * (D / C::KSQ) + (2 * wave + (lane >> 5)) * C::KWQ;
+    const int kwq = zq * (D / C::KSQ) + 2 * wave * C::KWQ, klq = kwq + (lane >> 5) * C::KWQ;
     const int cp = wg / C::KSP, zp = wg % C::KSP;
     constexpr int KCP = D / C::KSP;
-    const int klp = zp * KCP + (2 * wave + (lane >> 5)) * C::KWP;
-    if (cw && wg < C::NTQ) w_dma<C::KWQ>(wq, Lw.wqkv, D, 3 * D, cq * TN, klq - (lane >> 5) * C::KWQ, lane);
-    if (cw && wg < C::NTP) w_dma<C::KWP>(wp, Lw.wproj, D, D, cp * TN, klp - (lane >> 5) * C::KWP, lane);
+    const int kwp = zp * KCP + 2 * wave * C::KWP, klp = kwp + (lane >> 5) * C::KWP;
+    if (cw && wg < C::NTQ) w_dma<C::KWQ>(wq, Lw.wqkv, D, 3 * D, cq * TN, kwq, lane);
+    if (cw && wg < C::NTP) w_dma<C::KWP>(wp, Lw.wproj, D, D, cp * TN, kwp, lane);
 
     // ---- c_attn (LN1 output) -> P0 ----
     if (wg < C::NTQ) {
       wait_for(p, M, row_wg, E | seq_of(l - 1, PH_ROW3), 1);
       mark(l, PH_QKV, 0);
-      floatx16 acc;
+      floatx16 acc = {};  // (the poller wave passes zeros to tile_out)
       if (cw) {
-        float4 a[C::KWQ / 4];
-        a_rows<C::KWQ, FRESH>(a, xn1, D, M, klq, lane);
-        markv(l, PH_QKV, 1, a[C::KWQ / 4 - 1].w);
-        acc = mma_tile<C::KWQ>(a, wq, lane);
+        if constexpr (ADMA) {
+          float* aq = sm.h1.aq + wave * C::KWQ * 64;
+          a_dma<C::KWQ, FRESH>(aq, xn1, D, M, kwq, lane);
+          lds_dma_wait();
+          mark(l, PH_QKV, 1);
+          acc = mma_lds<C::KWQ>(aq, wq, lane);
+        } else {
+          float4 a[C::KWQ / 4];
+          a_rows<C::KWQ, FRESH>(a, xn1, D, M, klq, lane);
+          markv(l, PH_QKV, 1, a[C::KWQ / 4 - 1].w);
+          acc = mma_tile<C::KWQ>(a, wq, lane);
+        }
         markv(l, PH_QKV, 2, acc[15]);
       }
       const int n0 = cq * TN;
@@ -788,12 +886,20 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
           },
           E | seq_of(l, PH_ATT), 3);
       mark(l, PH_PROJ, 0);
-      floatx16 acc;
+      floatx16 acc = {};  // (the poller wave passes zeros to tile_out)
       if (cw) {
-        float4 a[C::KWP / 4];
-        a_rows<C::KWP, FRESH>(a, ol, D, M, klp, lane);
-        markv(l, PH_PROJ, 1, a[C::KWP / 4 - 1].w);
-        acc = mma_tile<C::KWP>(a, wp, lane);
+        if constexpr (ADMA) {
+          float* ap = sm.h1.wq + wave * C::KWP * 64;  // the c_attn weights are consumed
+          a_dma<C::KWP, FRESH>(ap, ol, D, M, kwp, lane);
+          lds_dma_wait();
+          mark(l, PH_PROJ, 1);
+          acc = mma_lds<C::KWP>(ap, wp, lane);
+        } else {
+          float4 a[C::KWP / 4];
+          a_rows<C::KWP, FRESH>(a, ol, D, M, klp, lane);
+          markv(l, PH_PROJ, 1, a[C::KWP / 4 - 1].w);
+          acc = mma_tile<C::KWP>(a, wp, lane);
+        }
         markv(l, PH_PROJ, 2, acc[15]);
       }
       const int n0 = cp * TN;
@@ -815,49 +921,98 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
       signal(p, E | seq_of(l, PH_ROW2));
       mark(l, PH_ROW2, 3);
     }
-    // weights of this layer's c_fc and mlp c_proj tiles, in flight from here (after the
-    // row workgroups' LayerNorm, whose registers they would otherwise share)
-    float* wf = sm.h2.wf + wave * C::KWF * 64;
-    float* wm = sm.h2.wm + wave * C::KWM * 64;
+    // c_fc weights (into LDS) in flight from here (after the row workgroups'
+    // LayerNorm, whose registers they would otherwise share); mlp c_proj's
+    // (into registers) once c_fc's stores are issued
+    float* wf = sm.h2.x + wave * C::KWF * 64;
     const int cf = wg / C::KSF, zf = wg % C::KSF;
-    const int klf = zf * (D / C::KSF) + (2 * wave + (lane >> 5)) * C::KWF;
+    const int kwf = zf * (D / C::KSF) + 2 * wave * C::KWF, klf = kwf + (lane >> 5) * C::KWF;
     const int cm = wg / C::KSM, zm = wg % C::KSM;
     constexpr int KCM = 4 * D / C::KSM;
-    const int klm = zm * KCM + (2 * wave + (lane >> 5)) * C::KWM;
-    if (cw && wg < C::NTF) w_dma<C::KWF>(wf, Lw.wfc, D, 4 * D, cf * TN, klf - (lane >> 5) * C::KWF, lane);
-    if (cw && wg < C::NTM) w_dma<C::KWM>(wm, Lw.wmlp, 4 * D, D, cm * TN, klm - (lane >> 5) * C::KWM, lane);
+    const int kwm = zm * KCM + 2 * wave * C::KWM, klm = kwm + (lane >> 5) * C::KWM;
+    float4 wm[C::KWM / 4];
+#pragma unroll
+    for (int j = 0; j < C::KWM / 4; ++j) wm[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (cw && wg < C::NTF) w_dma<C::KWF>(wf, Lw.wfc, D, 4 * D, cf * TN, kwf, lane);
     // ---- c_fc (LN2 output) -> P0 ----
     if (wg < C::NTF) {
       wait_for(p, M, row_wg, E | seq_of(l, PH_ROW2), 5);
       mark(l, PH_FC, 0);
-      floatx16 acc;
+      floatx16 acc = {};  // (the poller wave passes zeros to tile_out)
       if (cw) {
-        float4 a[C::KWF / 4];
-        a_rows<C::KWF, FRESH>(a, xn2, D, M, klf, lane);
-        markv(l, PH_FC, 1, a[C::KWF / 4 - 1].w);
-        acc = mma_tile<C::KWF>(a, wf, lane);
+        if constexpr (ADMA) {
+          float* af = sm.h2.x + RSmem<D>::WF + wave * C::KWF * 64;
+          a_dma<C::KWF, FRESH>(af, xn2, D, M, kwf, lane);
+          lds_dma_wait();
+          mark(l, PH_FC, 1);
+          acc = mma_lds<C::KWF>(af, wf, lane);
+        } else {
+          float4 a[C::KWF / 4];
+          a_rows<C::KWF, FRESH>(a, xn2, D, M, klf, lane);
+          markv(l, PH_FC, 1, a[C::KWF / 4 - 1].w);
+          acc = mma_tile<C::KWF>(a, wf, lane);
+        }
         markv(l, PH_FC, 2, acc[15]);
       }
       const int n0 = cf * TN;
       tile_out(acc, red, lane, [&](int r, int cc, float v) {
         if (r < M) stc(p0f + ((size_t)zf * MR + r) * (4 * D) + n0 + cc, v);
       });
-      signal(p, E | seq_of(l, PH_FC));
+      if (wg < C::NTM) {
+        if (cw) w_regs<C::KWM>(wm, Lw.wmlp, 4 * D, D, cm * TN, klm, lane);
+        signal_keep<C::KWM / 4>(p, E | seq_of(l, PH_FC));  // the partials, not the weights just issued
+      } else {
+        signal(p, E | seq_of(l, PH_FC));
+      }
       mark(l, PH_FC, 3);
     }
     // ---- mlp c_proj (gelu_new of the c_fc output) -> P1 ----
     if (wg < C::NTM) {
+      if (cw && wg >= C::NTF) w_regs<C::KWM>(wm, Lw.wmlp, 4 * D, D, cm * TN, klm, lane);
       // the c_fc tiles of columns [zm KCM, zm KCM + KCM), every k split
       wait_for(
           p, (KCM / TN) * C::KSF, [&](int i) { return (zm * (KCM / TN) + i / C::KSF) * C::KSF + i % C::KSF; },
           E | seq_of(l, PH_FC), 6);
       mark(l, PH_MLP, 0);
-      floatx16 acc;
+      floatx16 acc = {};  // (the poller wave passes zeros to tile_out)
       if (cw) {
-        float4 a[C::KWM / 4];
-        a_gelu<C::KWM, C::KSF, FRESH>(a, p0f, 4 * D, M, Lw.bfc, klm, lane);
-        markv(l, PH_MLP, 1, a[C::KWM / 4 - 1].w);
-        acc = mma_tile<C::KWM>(a, wm, lane);
+        if constexpr (ADMA) {
+          // the KSF partial slices into LDS (where c_fc's weights and
+          // activations were), summed in k order + bias, gelu_new, as read
+          float* am = sm.h2.x + wave * C::KWM * 64;
+#pragma unroll
+          for (int z = 0; z < C::KSF; ++z)
+            a_dma<C::KWM, FRESH>(am + z * RSmem<D>::WM, p0f + (size_t)z * MR * (4 * D), 4 * D, M, kwm, lane);
+          // the bias of the wave's k range (2 KWM values; lanes past it re-read its last chunk)
+          float* bl = sm.h2.x + C::KSF * RSmem<D>::WM + wave * 256;
+          lds_dma16<1>(Lw.bfc + kwm + 4 * min(lane, C::KWM / 2 - 1), bl);
+          lds_dma_wait();
+          mark(l, PH_MLP, 1);
+          floatx16 c0, c1;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) c0[e] = c1[e] = 0.f;
+#pragma unroll
+          for (int j = 0; j < C::KWM / 4; ++j) {
+            float4 t = w_chunk<C::KWM>(am, j, lane);
+#pragma unroll
+            for (int z = 1; z < C::KSF; ++z) t = add4(t, w_chunk<C::KWM>(am + z * RSmem<D>::WM, j, lane));
+            const float4 b = *reinterpret_cast<const float4*>(bl + (lane >> 5) * C::KWM + 4 * j);
+            const float4 av =
+                make_float4(gelu_new(t.x + b.x), gelu_new(t.y + b.y), gelu_new(t.z + b.z), gelu_new(t.w + b.w));
+            mma4(av, wm[j], c0, c1);
+          }
+          acc = c0 + c1;
+        } else {
+          float4 a[C::KWM / 4];
+          a_gelu<C::KWM, C::KSF, FRESH>(a, p0f, 4 * D, M, Lw.bfc, klm, lane);
+          markv(l, PH_MLP, 1, a[C::KWM / 4 - 1].w);
+          floatx16 c0, c1;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) c0[e] = c1[e] = 0.f;
+#pragma unroll
+          for (int j = 0; j < C::KWM / 4; ++j) mma4(a[j], wm[j], c0, c1);
+          acc = c0 + c1;
+        }
         markv(l, PH_MLP, 2, acc[15]);
       }
       const int n0 = cm * TN;
@@ -907,11 +1062,10 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
 #pragma unroll
       for (int st = 0; st < NS; ++st) a_rows<16, FRESH>(a[st], xn_of(2 * L), D, M, 128 * st + 32 * wave + 16 * (lane >> 5), lane);
     }
+    u64 best[4] = {0ull, 0ull, 0ull, 0ull};  // argmax keys of this thread's rows (greedy finish)
     for (int g0 = 0; g0 < nst; g0 += NS) {
-      floatx16 c0, c1;
+      floatx16 c0 = {}, c1 = {};
       if (cw) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) c0[e] = c1[e] = 0.f;
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
           const int g = g0 + st;
@@ -925,8 +1079,33 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
       }
       const int n0 = (wg + (g0 / NS) * G) * TN;
       tile_out(c0 + c1, red, lane, [&](int r, int cc, float v) {
-        if (r < M && n0 + cc < p.V) p.logits[(size_t)r * p.V + n0 + cc] = v;
+        if (r < M && n0 + cc < p.V) {
+          p.logits[(size_t)r * p.V + n0 + cc] = v;
+          const u64 k = argmax_key(v, (uint32_t)(n0 + cc));
+          best[r & 3] = k > best[r & 3] ? k : best[r & 3];
+        }
       });
+    }
+    if (p.keys != nullptr && cw) {
+      // per row: the max over the 32 lanes of its half-wave, one device-scope
+      // atomic max per workgroup for each sequence's last row; its returned
+      // value is consumed so that the max has been performed before this
+      // workgroup counts itself done
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        u64 b = best[u];
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) {
+          const u64 o = __shfl_xor(b, off, 64);
+          b = o > b ? o : b;
+        }
+        const int r = 8 * wave + 4 * (lane >> 5) + u;
+        if ((lane & 31) == 0 && r < M && r % T == T - 1 && b != 0ull) {
+          const u64 prev = __hip_atomic_fetch_max(RK_GW(u64, p.keys + r / T), b, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+          asm volatile("" : : "v"(prev));
+        }
+      }
     }
     mark(L, PH_QKV, 3);
   }
@@ -942,6 +1121,18 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
     const unsigned old =
         __hip_atomic_fetch_add(RK_GW(unsigned, p.done), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == G - 1) {
+      if (p.keys != nullptr) {
+        const int step = *RK_G(int, p.step);
+        for (int sq = 0; sq < S; ++sq) {
+          const u64 k = __hip_atomic_load(RK_GW(u64, p.keys + sq), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const uint32_t t = argmax_key_index(k);
+          p.token[sq] = t;
+          if (p.ids_out) p.ids_out[(size_t)sq * p.ld_ids + step] = t;
+          p.keys[sq] = 0ull;
+        }
+        *p.fin_pos = *p.fin_pos + 1;
+        *p.step = step + 1;
+      }
       __hip_atomic_store(RK_GW(unsigned, p.done), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(RK_GW(u64, p.epoch), (E >> 16) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

@@ -542,10 +542,10 @@ static void enqueue_decode_step(rtg_cache* c, int pos = -1) {
     launch_finalize(s, B, c->keys, c->token_dev, c->ids_dev, P, c->pos_dev, c->step_dev, nullptr);
 }
 
+// Device-side fills (no staging copy of a host value); never captured.
 static void set_counters(rtg_cache* c, int pos, int step) {
-  int hv[2] = {pos, step};
-  HIPX(hipMemcpyAsync(c->pos_dev, &hv[0], 4, hipMemcpyHostToDevice, c->stream));
-  HIPX(hipMemcpyAsync(c->step_dev, &hv[1], 4, hipMemcpyHostToDevice, c->stream));
+  HIPX(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(c->pos_dev), pos, 1, c->stream));
+  HIPX(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(c->step_dev), step, 1, c->stream));
 }
 
 // The multi-row forward runs S sequences x T tokens of a cache of batch S in
@@ -560,7 +560,7 @@ static bool rows_path(const rtg_cache* c, size_t S, size_t T) {
 // persistent_launch_lock until the stream drains): ids_dev [S*T] at position
 // past, logits [S*T][V]; state st (default: the cache's own, made on first use).
 static void enqueue_rows(rtg_cache* c, const uint32_t* ids_dev, size_t S, size_t T, size_t past, float* logits,
-                         RowsState* st = nullptr) {
+                         RowsState* st = nullptr, const RowsFinish* fin = nullptr) {
   const rtg_model* m = c->m;
   if (!st) {
     if (!c->rstate) {
@@ -570,7 +570,7 @@ static void enqueue_rows(rtg_cache* c, const uint32_t* ids_dev, size_t S, size_t
     st = c->rstate;
   }
   HIPX(rows_forward(m->rplan, st, c->stream, c->k, c->v, (long)c->layer_stride, ids_dev, (int)S, (int)T, (int)past,
-                    nullptr, logits));
+                    nullptr, logits, fin));
 }
 
 // After the stream has drained: a bounded wait of the multi-row forward that
@@ -734,14 +734,20 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   if (c->pstate || rows) plock = std::unique_lock<std::mutex>(persistent_launch_lock(m->device));
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
   HIPX(hipEventRecord(c->ev[0], s));
-  if (rows) enqueue_rows(c, c->ids_in, B, n, 0, c->logits);
-  else enqueue_prefill(c, cache_work(c), c->ids_in, B, n, 0, 0);
-  // argmax of the last row of each sequence (extract_row(logits, n-1))
-  launch_argmax(s, c->logits + (n - 1) * V, (long)(n * V), (int)B, (int)V, c->keys);
   // finalize advances pos by one: after it, pos = n, the position of the
   // prefill token that the first decode step consumes.
   set_counters(c, (int)n - 1, 0);
-  launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev);
+  if (rows) {
+    // the prefill with the argmax of each sequence's last row and the
+    // finalize in the same launch
+    const RowsFinish fin{c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev};
+    enqueue_rows(c, c->ids_in, B, n, 0, c->logits, nullptr, &fin);
+  } else {
+    enqueue_prefill(c, cache_work(c), c->ids_in, B, n, 0, 0);
+    // argmax of the last row of each sequence (extract_row(logits, n-1))
+    launch_argmax(s, c->logits + (n - 1) * V, (long)(n * V), (int)B, (int)V, c->keys);
+    launch_finalize(s, (int)B, c->keys, c->token_dev, c->ids_dev, (int)P, c->pos_dev, c->step_dev);
+  }
   sample(c->logits + (n - 1) * V);
   HIPX(hipEventRecord(c->ev[1], s));
   // The persistent step (one kernel) is launched directly: replaying it as a
