@@ -145,18 +145,21 @@ rtg_result rtg_forward(const rtg_model* model, const uint32_t* ids, size_t n, fl
  * (may be NULL to skip the device-to-host copy). The cache must have batch 1
  * and belong to model. One new token (n == 1) runs the persistent decode
  * step that generate_cached runs per token, where the model's shape has one;
- * more tokens run the prefill kernels. */
+ * 2..32 tokens run the multi-row forward in one launch (f32 weights, n_embd
+ * 128, 768 or 1024); more tokens run the prefill kernels. */
 rtg_result rtg_forward_cached(const rtg_model* model, rtg_cache* cache, const uint32_t* ids, size_t n,
                               float* logits_out);
 /* forward_cached without device allocation. No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
- * arguments as rtg_forward_cached and the kernels of its prefill path (for
- * n >= 2 the same results bit for bit; for n == 1 rtg_forward_cached runs
- * the persistent decode step instead, and the two agree within the logits
- * tolerance), but the activations and logits of the pass live in a fixed
- * 16 MiB scratch array per device inside the library instead of the cache's
- * work buffers, and nothing is allocated. Limit: n * (10 * n_embd +
+ * arguments as rtg_forward_cached and the kernels of its path for n >= 2
+ * (the same results bit for bit; for n == 1 rtg_forward_cached runs the
+ * persistent decode step instead, and the two agree within the logits
+ * tolerance), but the pass's work rows and logits live in a fixed scratch
+ * array of 16 MiB + 64 KiB per device inside the library instead of the
+ * cache's buffers, and nothing is allocated. Up to 32 tokens run the
+ * multi-row forward (its flags and epoch in the 64 KiB, kept between calls);
+ * more run the prefill kernels, with the limit: n * (10 * n_embd +
  * vocab_size) floats (each of the six parts rounded up to 64) must fit in
  * 16 MiB, e.g. n <= 72 for GPT-2 small, n <= 63 for XL; a larger n returns
  * an error. The prefill GEMMs' split-k partials take what is left of the

@@ -524,16 +524,14 @@ __device__ __forceinline__ void row_resid(float4 (&x)[RCfg<D>::NU], const float*
 
 // ---------------------------------------------------------------------------
 // attention items (multi_head_attention_cached, gpt2.rs:772-834): item =
-// (sequence s, head h, query group g): queries t in [g QG, g QG + QG) of T > 1
-// new rows (one per compute wave), or the one query of T = 1 (its key range
-// split over the compute waves)
+// (sequence s, head h, query group g): queries t in [g QG, g QG + QG) of the T
+// new rows, one per compute wave
 // ---------------------------------------------------------------------------
 
 struct AttLds {
   float q[TMAX * HD];
   float k[TMAX * (HD + 4)];  // padded rows: lane-per-key reads spread over the banks
   float v[TMAX * HD];
-  float m[NCW * (HD + 2)];   // per-wave (m, l, o[64]) for the one-query merge
 };
 
 // One block of up to 64 keys [kb, kb + nk) of query t, keys from the cache
@@ -590,8 +588,8 @@ __device__ __forceinline__ void att_block(const AttLds& A, int t, int past, cons
   m = mn;
 }
 
-// Keys [0, k_hi) of query t in blocks of 64, block b0, b0 + bstep, ...: the
-// cache rows below past, then the new rows.
+// Keys [0, k_hi) of query t in blocks of 64 (b0, b0 + bstep, ...): the cache
+// rows below past, then the new rows.
 __device__ __forceinline__ void att_range(const AttLds& A, int t, int past, const float* Kc, const float* Vc,
                                           int k_hi, int b0, int bstep, float& m, float& l, float& o, int lane) {
   const int nb_c = (past + 63) / 64;              // blocks over the cache rows
@@ -731,7 +729,7 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
   const int M = p.M, S = p.S, T = p.T, L = p.L;
   const int past = p.pos_dev ? *RK_G(int, p.pos_dev) : p.past;
   const int my_row = wg >= G - M ? G - 1 - wg : -1;
-  const int ngr = T == 1 ? 1 : (T + QG - 1) / QG;  // query groups per (sequence, head)
+  const int ngr = (T + QG - 1) / QG;  // query groups per (sequence, head)
   const int my_item = G - 1 - wg < S * H * ngr ? G - 1 - wg : -1;
   const bool tracing = p.trace != nullptr && (L + 2) * 32 < TRACE_WORDS;
   if (tracing)
@@ -826,7 +824,7 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
     // ---- attention items ----
     if (my_item >= 0) {
       const int g = my_item % ngr, sh = my_item / ngr, s = sh / H, h = sh % H;
-      const int t_lo = T == 1 ? 0 : g * QG, t_hi = T == 1 ? 1 : min(T, g * QG + QG);
+      const int t_lo = g * QG, t_hi = min(T, g * QG + QG);
       // the c_attn tiles of head h's q, k and v columns
       auto prod = [&](int i) {
         const int z = i % C::KSQ, j = i / C::KSQ;  // j < 6: part j / 2, column tile 2h + j % 2
@@ -839,32 +837,7 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
       if (cw) att_gather<D, FRESH>(p, att, p0q, l, s, h, t_lo, t_hi, past, Kc, Vc, tid);
       __syncthreads();
       mark(l, PH_ATT, 1);
-      if (T == 1) {
-        // one query: the compute waves split the key blocks, then wave 0 merges
-        if (cw) {
-          float m = -__builtin_inff(), ll = 0.f, o = 0.f;
-          att_range(att, 0, past, Kc, Vc, past + 1, wave, NCW, m, ll, o, lane);
-          att.m[wave * (HD + 2) + 2 + lane] = o;
-          if (lane == 0) {
-            att.m[wave * (HD + 2)] = m;
-            att.m[wave * (HD + 2) + 1] = ll;
-          }
-        }
-        __syncthreads();
-        if (wave == 0) {
-          float mm = att.m[0];
-#pragma unroll
-          for (int w = 1; w < NCW; ++w) mm = fmaxf(mm, att.m[w * (HD + 2)]);
-          float lt = 0.f, ot = 0.f;
-#pragma unroll
-          for (int w = 0; w < NCW; ++w) {
-            const float f = fexp_a(att.m[w * (HD + 2)] - mm);
-            lt += att.m[w * (HD + 2) + 1] * f;
-            ot += att.m[w * (HD + 2) + 2 + lane] * f;
-          }
-          stc(ol + (size_t)s * D + h * HD + lane, ot / lt);
-        }
-      } else if (cw && t_lo + wave < t_hi) {
+      if (cw && t_lo + wave < t_hi) {
         const int t = t_lo + wave;
         float m = -__builtin_inff(), ll = 0.f, o = 0.f;
         att_range(att, t, past, Kc, Vc, past + t + 1, 0, 1, m, ll, o, lane);

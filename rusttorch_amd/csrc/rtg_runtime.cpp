@@ -730,6 +730,10 @@ static void generate_greedy(const rtg_model* m, const uint32_t* prompts, size_t 
   // step of this process may be in flight on the device (another thread's
   // cache) until this stream has drained.
   const bool rows = rows_path(c, B, n);
+  if (rows && !c->rstate) {  // (allocated before the timed prefill)
+    c->rstate = rows_state_create(m->rplan);
+    if (!c->rstate) throw HipError{"multi-row forward: state allocation failed"};
+  }
   std::unique_lock<std::mutex> plock;
   if (c->pstate || rows) plock = std::unique_lock<std::mutex>(persistent_launch_lock(m->device));
   HIPX(hipMemcpyAsync(c->ids_in, prompts, B * n * 4, hipMemcpyHostToDevice, s));
