@@ -47,7 +47,8 @@ unsigned* rows_err(RowsState* s);
 // With fin set, the launch also finishes a greedy step the way launch_argmax
 // + launch_finalize do: keys [S] (zero on entry, cleared again), the argmax
 // token of each sequence's last row into token [S] and ids_out[s * ld_ids +
-// *step], then *pos and *step advanced by one.
+// *step], then *pos and *step advanced by one; for S <= 4 it then computes
+// only those last rows' logits (the other rows of logits are not written).
 struct RowsFinish {
   unsigned long long* keys;
   uint32_t* token;

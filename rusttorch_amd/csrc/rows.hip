@@ -184,6 +184,7 @@ hipError_t rows_forward(const RowsPlan* p, RowsState* s, hipStream_t stream, flo
   a.logits = logits;
   if (fin) {
     a.keys = fin->keys;
+    a.lm_last = S <= rk::LM_LAST_MAX;
     a.token = fin->token;
     a.ids_out = fin->ids_out;
     a.ld_ids = fin->ld_ids;

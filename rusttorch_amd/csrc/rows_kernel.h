@@ -143,6 +143,7 @@ struct RParams {
   // the keys and advances *fin_pos and *step by one (the finalize of the
   // reference's generate loop, gpt2.rs:431-437).
   unsigned long long* keys;
+  int lm_last;  // set (with keys, S <= LM_LAST_MAX): the LM head computes only each sequence's last row
   uint32_t* token;
   uint32_t* ids_out;
   int ld_ids;
@@ -290,6 +291,7 @@ __device__ __forceinline__ void lds_dma16(const float* src, float* dst) {
 __device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 constexpr int LM_RING = 6;  // LM head weight slices in flight per wave (4 KiB each)
+constexpr int LM_LAST_MAX = 4;  // sequences of the last-row LM head
 // Waits until at most 4 n of this wave's memory instructions are outstanding
 // (n = later LM head slices in flight, 4 DMA instructions each).
 __device__ __forceinline__ void lm_wait(int n) {
@@ -1011,6 +1013,81 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
     }
   }
 
+  // ---- the LM head for each sequence's last row only (generate_cached reads
+  // nothing else of its prefill's logits, gpt2.rs:420-423): a GEMV streaming
+  // wte once, workgroup wg taking vocabulary rows [wg VPW, wg VPW + VPW),
+  // compute wave w every 4th of them, lane l holding columns 4 (l + 64 u) of
+  // a row; batches of 4 rows double-buffered in registers ----
+  if (p.lm_last) {
+    const int lane = tid0 & 63;
+    constexpr int NC = D / 4, RB = 4;
+    wait_for(p, M, row_wg, E | seq_of(L - 1, PH_ROW3), 8);
+    mark(L, PH_QKV, 0);
+    const int VPW = (p.V + G - 1) / G, v0 = wg * VPW, v1 = min(p.V, v0 + VPW);
+    const int nr = v1 > v0 + wave ? (v1 - v0 - wave + NCW - 1) / NCW : 0;  // this wave's rows
+    u64 bk[LM_LAST_MAX] = {0ull, 0ull, 0ull, 0ull};
+    if (cw && nr > 0) {
+      float4 xs[LM_LAST_MAX][NU];
+#pragma unroll
+      for (int sq = 0; sq < LM_LAST_MAX; ++sq)
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          xs[sq][u] = sq < S ? ldx4<FRESH>(xn_of(2 * L) + (size_t)(sq * T + T - 1) * D + 4 * min(lane + 64 * u, NC - 1))
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 wa[RB][NU], wb[RB][NU];
+      auto load = [&](int b, float4 (&w)[RB][NU]) {
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+          const int v = v0 + wave + NCW * min(RB * b + j, nr - 1);
+#pragma unroll
+          for (int u = 0; u < NU; ++u) w[j][u] = ldnt4(p.wte + (size_t)v * D + 4 * min(lane + 64 * u, NC - 1));
+        }
+      };
+      auto use = [&](int b, const float4 (&w)[RB][NU]) {
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+          const int i = RB * b + j;
+          if (i >= nr) break;  // wave-uniform
+          const int v = v0 + wave + NCW * i;
+#pragma unroll
+          for (int sq = 0; sq < LM_LAST_MAX; ++sq) {
+            if (sq >= S) break;
+            float d = 0.f;
+#pragma unroll
+            for (int u = 0; u < NU; ++u)
+              if (lane + 64 * u < NC)
+                d += w[j][u].x * xs[sq][u].x + w[j][u].y * xs[sq][u].y + w[j][u].z * xs[sq][u].z +
+                     w[j][u].w * xs[sq][u].w;
+            d = wsum(d);  // the whole sum in every lane
+            if (lane == sq) *RK_GW(float, p.logits + (size_t)(sq * T + T - 1) * p.V + v) = d;
+            const u64 k = argmax_key(d, (uint32_t)v);
+            bk[sq] = k > bk[sq] ? k : bk[sq];
+          }
+        }
+      };
+      const int nb = (nr + RB - 1) / RB;
+      load(0, wa);
+      if (nb > 1) load(1, wb);
+      for (int b = 0; b < nb; b += 2) {
+        use(b, wa);
+        if (b + 2 < nb) load(b + 2, wa);
+        if (b + 1 < nb) {
+          use(b + 1, wb);
+          if (b + 3 < nb) load(b + 3, wb);
+        }
+      }
+    }
+    // lane s adds sequence s's best key (the same in every lane) to keys[s];
+    // the returned value is consumed so that the max has been performed
+    // before this workgroup counts itself done
+    const u64 b = lane == 0 ? bk[0] : lane == 1 ? bk[1] : lane == 2 ? bk[2] : bk[3];
+    if (cw && lane < S && b != 0ull) {
+      const u64 prev =
+          __hip_atomic_fetch_max(RK_GW(u64, p.keys + lane), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("" : : "v"(prev));
+    }
+    mark(L, PH_QKV, 3);
+  } else
   // ---- tied LM head (gpt2.rs:392-396): logits[r][n] = ln_f(x_r) . wte[n] ----
   // Tiles of 32 vocabulary rows, workgroup wg taking tiles wg, wg + G, ...;
   // each tile in NS = D / 128 k steps, compute wave w taking k [128 s + 32 w,
