@@ -15,8 +15,10 @@
 
 namespace rtg {
 namespace pk {
-// Kernel instances, one per (width, vocabulary, weight storage); defined in
-// the decode_persistent_inst_*.hip files.
+// Kernel instances, one per (width, largest vocabulary, weight storage);
+// defined in the decode_persistent_inst_*.hip files. A model whose vocabulary
+// is at most an instance's runs on it (the LM head's rows then go to fewer
+// workgroups).
 const void* kernel_128_512_f32();
 const void* kernel_128_512_bf16();
 const void* kernel_768_50257_f32();
@@ -105,7 +107,7 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   if (H <= 0 || d != H * pk::HD || L <= 0 || P <= 0) return pl;
   const void* fn = nullptr;
   for (const Inst& in : kInstances)
-    if (in.d == d && in.v == V && in.wtype == w.wtype) fn = in.fn();
+    if (in.d == d && V >= 1 && V <= in.v && in.wtype == w.wtype) fn = in.fn();
   if (!fn) return pl;
   // folded constants: per layer sq, cq [3d] and sf, cf [4d]; then sl, cl [V]
   const size_t per_layer = 2 * (size_t)(3 * d) + 2 * (size_t)(4 * d);
@@ -141,6 +143,7 @@ PersistentPlan* persistent_plan_create(const PersistentWeights& w) {
   p.cl = cl;
   p.L = L;
   p.P = P;
+  p.V = V;
   p.eps = w.cfg.layer_norm_epsilon;
   p.kv_layer = (long)H * P * pk::HD;
   // Tagged exchange regions of one layer: one slot of whole 128-byte lines per

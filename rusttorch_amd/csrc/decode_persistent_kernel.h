@@ -93,6 +93,8 @@ struct Params {
   const float *wpe, *lnfw, *lnfb;
   const float *sl, *cl;  // ln_f folded into the tied LM head, as for the layers
   int L, P;
+  int V;  // vocabulary rows of the LM head (at most the instance's compiled V; the rows go to the first
+          // ceil(V / RPW) workgroups)
   float eps;
   float* kc;  // [L][H][P][HD]
   float* vc;
@@ -350,10 +352,10 @@ struct V16<W_BF16> {
 template <int WT, int MAXSEG, class GEO, int PACE = PK_PACE, bool NT = PK_W_NT>
 __device__ __forceinline__ void seg_issue(typename V16<WT>::T (&buf)[MAXSEG], const void* W, const void* dummy, int wg,
                                           int cw, int lane, int seg_base, unsigned* ready = nullptr,
-                                          unsigned next = 0) {
+                                          unsigned next = 0, int n_rows = GEO::N) {
   typedef typename V16<WT>::T Vec;
   const int row0 = wg * GEO::RPW;
-  const int rows_here = min(GEO::RPW, GEO::N - row0);
+  const int rows_here = min(GEO::RPW, n_rows - row0);
   const int segs_here = rows_here > 0 ? rows_here * GEO::SPR : 0;
   const int s0 = seg_base + cw * GEO::SPW;
   const int nseg = min(GEO::SPW, segs_here - s0);
@@ -407,11 +409,11 @@ __device__ __forceinline__ float wave_sum_all(float v) {
 // row's slots add up to its dot product.
 template <int WT, int MAXSEG, class GEO>
 __device__ __forceinline__ void seg_compute(const typename V16<WT>::T (&buf)[MAXSEG], const float* x, float* part,
-                                            int wg, int cw, int lane, int seg_base) {
+                                            int wg, int cw, int lane, int seg_base, int n_rows = GEO::N) {
   constexpr int E = V16<WT>::E, SPR = GEO::SPR, SPW = GEO::SPW;
   constexpr int NPC = GEO::ALIGNED ? SPW / SPR : (SPW + SPR - 2) / SPR + 1;
   const int row0 = wg * GEO::RPW;
-  const int rows_here = min(GEO::RPW, GEO::N - row0);
+  const int rows_here = min(GEO::RPW, n_rows - row0);
   const int segs_here = rows_here > 0 ? rows_here * SPR : 0;
   const int s0 = seg_base + cw * SPW;
   const int nseg = min(SPW, segs_here - s0);
@@ -512,23 +514,23 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);
     seg_issue<WT, MS, GM, C::PACE>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
     compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);
-    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
+    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1, p.V);
     compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);
-    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE);
+    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE, p.V);
   }
   // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
   // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
   lds_wait_ge(&sm.in_ready[PH_LM], NGLUE, p.err);
   ++seq;
   constexpr int PER_CHUNK = NC * GL::SPW;
-  const int rows_here = min(GL::RPW, GL::N - wg * GL::RPW);
+  const int rows_here = min(GL::RPW, p.V - wg * GL::RPW);
   const int segs_here = rows_here > 0 ? rows_here * GL::SPR : 0;
   for (int base = 0; base < segs_here; base += 2 * PER_CHUNK) {
     // nothing else is in flight now: stream at full rate
-    seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base);
-    seg_issue<WT, MS, GL, 0, C::LM_NT>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK);
-    seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK);
-    seg_issue<WT, MS, GL, 0, C::LM_NT>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK);
+    seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base, p.V);
+    seg_issue<WT, MS, GL, 0, C::LM_NT>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK, nullptr, 0, p.V);
+    seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK, p.V);
+    seg_issue<WT, MS, GL, 0, C::LM_NT>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK, nullptr, 0, p.V);
   }
   lds_release();
   if (lane == 0) lds_add(&sm.gemv_done, 1);
@@ -1086,7 +1088,7 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
   }
   // ---- ln_f + tied LM head + argmax (gpt2.rs:392-396, 858-868), ln_f folded ----
   constexpr int NLR = (GL::RPW + 63) / 64;  // LM-head rows per leader lane
-  const int row0 = wg * GL::RPW, rows_here = min(GL::RPW, GL::N - row0);
+  const int row0 = wg * GL::RPW, rows_here = min(GL::RPW, p.V - row0);
   float sl[NLR], cl[NLR];
 #pragma unroll
   for (int k = 0; k < NLR; ++k) {

@@ -121,6 +121,28 @@ def test_wide_persistent_step_logits(oracle_lib, name, storage, steps):
     m.close()
 
 
+@pytest.mark.parametrize("vocab,d,heads", [(1000, 768, 12), (300, 128, 2)])
+def test_persistent_step_smaller_vocabulary(oracle_lib, monkeypatch, tmp_path, vocab, d, heads):
+    """A vocabulary below the one a persistent instance is compiled for
+    (50257 at d = 768, 512 at d = 128) runs on that instance, the LM head's
+    rows on the first workgroups only: every decode step's logits against
+    the oracle, and the persistent step is the one that ran (it writes its
+    phase trace when RTG_TRACE_FILE is set)."""
+    sh = synth.ModelShape(vocab, 128, d, 2, heads)
+    sd = synth.make_weights(sh)
+    trace = tmp_path / "trace.bin"
+    monkeypatch.setenv("RTG_TRACE_FILE", str(trace))
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    om = oracle_lib.OracleModel.from_shape(sd, sh, threads=THREADS)
+    prompt = synth.make_tokens(20, vocab, stream=690)
+    ids = m.generate_cached(prompt, 17, 0.0)
+    assert trace.exists(), "the persistent step did not run"
+    worst, diffs = _steps_against_oracle(om, m, ids, 20, set(range(16)), f"V={vocab} d={d}")
+    assert len(diffs) == 16
+    print(f"[gpu] V={vocab} d={d} persistent step: 16 decode steps, max |d| {worst:.3e}", flush=True)
+    m.close()
+
+
 def test_small_generate_equals_generate_cached():
     """The reference harness's check at model size (examples/gpt2_bench.rs:
     53-70): GPT-2 small, uncached generate (a full forward over the window
