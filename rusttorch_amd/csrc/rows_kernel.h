@@ -337,16 +337,6 @@ template <int KW, bool FRESH>
 __device__ __forceinline__ void a_dma(float* al, const float* X, int ldx, int M, int kw0, int lane) {
   w_dma<KW, FRESH ? 1 : 2>(al, X, ldx, M, 0, kw0, lane);
 }
-// Every wave's vector memory instructions except its last n have completed,
-// then the workgroup barrier; one lane publishes the flag.
-template <int N>
-__device__ __forceinline__ void signal_keep(const RParams& p, u64 val) {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-  __syncthreads();
-  if (threadIdx.x == 0)
-    __hip_atomic_store(RK_GW(u64, p.flags + (size_t)blockIdx.x * FS), val, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
 
 template <int KW, bool FRESH>
 __device__ __forceinline__ void a_rows(float4 (&a)[KW / 4], const float* X, int ldx, int M, int kl, int lane) {
@@ -933,12 +923,11 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
       tile_out(acc, red, lane, [&](int r, int cc, float v) {
         if (r < M) stc(p0f + ((size_t)zf * MR + r) * (4 * D) + n0 + cc, v);
       });
-      if (wg < C::NTM) {
-        if (cw) w_regs<C::KWM>(wm, Lw.wmlp, 4 * D, D, cm * TN, klm, lane);
-        signal_keep<C::KWM / 4>(p, E | seq_of(l, PH_FC));  // the partials, not the weights just issued
-      } else {
-        signal(p, E | seq_of(l, PH_FC));
-      }
+      signal(p, E | seq_of(l, PH_FC));
+      // mlp c_proj's weights once the partials are published (the flag
+      // waits for every memory instruction of the wave, in whatever order
+      // loads and stores complete)
+      if (wg < C::NTM && cw) w_regs<C::KWM>(wm, Lw.wmlp, 4 * D, D, cm * TN, klm, lane);
       mark(l, PH_FC, 3);
     }
     // ---- mlp c_proj (gelu_new of the c_fc output) -> P1 ----
