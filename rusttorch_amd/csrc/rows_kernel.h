@@ -455,11 +455,19 @@ __device__ __forceinline__ void tile_out(const floatx16& acc, float* red, int la
 // rows: residual add of a GEMM's partials and the LayerNorm after it
 // ---------------------------------------------------------------------------
 
-// LayerNorm of the row in x (gpt2.rs:636-666: mean, then the mean of squared
-// deviations, (x - mean) / sqrt(var + eps) * g + b) into row xn_row.
+// A row's NU 16-byte chunks of v (lane's chunks lane + 64 u, clamped).
 template <int D>
-__device__ __forceinline__ void row_ln(const float4 (&x)[RCfg<D>::NU], const float* g, const float* b, float eps,
-                                       float* xn_row, int lane) {
+__device__ __forceinline__ void row_load(float4 (&r)[RCfg<D>::NU], const float* v, int lane) {
+#pragma unroll
+  for (int u = 0; u < RCfg<D>::NU; ++u) r[u] = ld4(v + 4 * min(lane + 64 * u, D / 4 - 1));
+}
+
+// LayerNorm of the row in x (gpt2.rs:636-666: mean, then the mean of squared
+// deviations, (x - mean) / sqrt(var + eps) * g + b) into row xn_row; gv, bv:
+// the gain and bias chunks (row_load), loaded ahead.
+template <int D>
+__device__ __forceinline__ void row_ln(const float4 (&x)[RCfg<D>::NU], const float4 (&gv)[RCfg<D>::NU],
+                                       const float4 (&bv)[RCfg<D>::NU], float eps, float* xn_row, int lane) {
   constexpr int NU = RCfg<D>::NU, NC = D / 4;
   float sum = 0.f;
 #pragma unroll
@@ -478,20 +486,20 @@ __device__ __forceinline__ void row_ln(const float4 (&x)[RCfg<D>::NU], const flo
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
     const int ch = lane + 64 * u;
-    if (ch < NC) {
-      const float4 gv = ld4(g + 4 * ch), bv = ld4(b + 4 * ch);
-      stc4(xn_row + 4 * ch,
-           make_float4((x[u].x - mean) * inv_std * gv.x + bv.x, (x[u].y - mean) * inv_std * gv.y + bv.y,
-                       (x[u].z - mean) * inv_std * gv.z + bv.z, (x[u].w - mean) * inv_std * gv.w + bv.w));
-    }
+    if (ch < NC)
+      stc4(xn_row + 4 * ch, make_float4((x[u].x - mean) * inv_std * gv[u].x + bv[u].x,
+                                        (x[u].y - mean) * inv_std * gv[u].y + bv[u].y,
+                                        (x[u].z - mean) * inv_std * gv[u].z + bv[u].z,
+                                        (x[u].w - mean) * inv_std * gv[u].w + bv[u].w));
   }
 }
 
 // x += (sum of the KS partial rows in k order) + bias (gpt2.rs:517-537: the
-// residual add of the projection's output, bias included).
+// residual add of the projection's output, bias included; bias: row_load's
+// chunks, loaded ahead).
 template <int D, int KS>
-__device__ __forceinline__ void row_resid(float4 (&x)[RCfg<D>::NU], const float* P, int r, const float* bias,
-                                          int lane) {
+__device__ __forceinline__ void row_resid(float4 (&x)[RCfg<D>::NU], const float* P, int r,
+                                          const float4 (&bias)[RCfg<D>::NU], int lane) {
   constexpr int NU = RCfg<D>::NU, NC = D / 4;
   float4 t[KS][NU];
 #pragma unroll
@@ -508,7 +516,7 @@ __device__ __forceinline__ void row_resid(float4 (&x)[RCfg<D>::NU], const float*
       float4 s = t[0][u];
 #pragma unroll
       for (int z = 1; z < KS; ++z) s = add4(s, t[z][u]);
-      const float4 b = ld4(bias + 4 * ch);
+      const float4 b = bias[u];
       x[u] = add4(x[u], make_float4(s.x + b.x, s.y + b.y, s.z + b.z, s.w + b.w));
     }
   }
@@ -622,7 +630,7 @@ __device__ __forceinline__ void att_gather(const RParams& p, AttLds& A, const fl
       d4 = f % (HD / 4);
     }
   };
-  float4 v[EMAX][KS];
+  float4 v[EMAX][KS], bb[EMAX];
 #pragma unroll
   for (int i = 0; i < EMAX; ++i) {
     const int e = tid + NCT * i;
@@ -632,6 +640,7 @@ __device__ __forceinline__ void att_gather(const RParams& p, AttLds& A, const fl
       const int col = part * D + h * HD + 4 * d4, r = s * T + t;
 #pragma unroll
       for (int z = 0; z < KS; ++z) v[i][z] = ldx4<FRESH>(P0 + ((size_t)z * MR + r) * (3 * D) + col);
+      bb[i] = ld4(bq + col);  // with the partials, not a round trip after them
     }
   }
 #pragma unroll
@@ -644,7 +653,7 @@ __device__ __forceinline__ void att_gather(const RParams& p, AttLds& A, const fl
       float4 sum = v[i][0];
 #pragma unroll
       for (int z = 1; z < KS; ++z) sum = add4(sum, v[i][z]);
-      const float4 b = ld4(bq + col);
+      const float4 b = bb[i];
       const float4 x = make_float4(sum.x + b.x, sum.y + b.y, sum.z + b.z, sum.w + b.w);
       if (part == 0) {
         *reinterpret_cast<float4*>(A.q + t * HD + 4 * d4) = x;
@@ -711,6 +720,9 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
   __shared__ RSmem<D> sm;
   static_assert(sizeof(RSmem<D>) <= 160 * 1024, "LDS");
   constexpr bool ADMA = RSmem<D>::ADMA;
+  // row phases load their bias and LayerNorm rows before waiting (registers
+  // allow it up to 768 wide; wider rows load them with the partials)
+  constexpr bool RPF = D <= 768;
   static_assert(!ADMA || C::KWP <= C::KWQ, "attn c_proj activations in the c_attn weight region");
   float* red = sm.red;
   AttLds& att = sm.h1.att;
@@ -753,9 +765,10 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
         const int ch = min(lane + 64 * u, D / 4 - 1);
         xr[u] = add4(ld4(p.wte + (size_t)id * D + 4 * ch), ld4(p.wpe + (size_t)pos * D + 4 * ch));
       }
-      const float* g = L ? p.layers[0].ln1w : p.lnfw;
-      const float* b = L ? p.layers[0].ln1b : p.lnfb;
-      row_ln<D>(xr, g, b, p.eps, xn_of(0) + (size_t)my_row * D, lane);
+      float4 gv[NU], bv[NU];
+      row_load<D>(gv, L ? p.layers[0].ln1w : p.lnfw, lane);
+      row_load<D>(bv, L ? p.layers[0].ln1b : p.lnfb, lane);
+      row_ln<D>(xr, gv, bv, p.eps, xn_of(0) + (size_t)my_row * D, lane);
     }
     signal(p, E | seq_of(-1, PH_ROW3));
     mark(-1, PH_ROW3, 3);
@@ -876,12 +889,22 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
     }
     // ---- x += attention output; LN2 -> XN ----
     if (my_row >= 0) {
+      // the bias, gain and LN bias rows: before the wait where the registers
+      // allow (they do not depend on it), else with the partials
+      float4 bv[NU], gv[NU], lv[NU];
+      auto params = [&] {
+        row_load<D>(bv, Lw.bproj, lane);
+        row_load<D>(gv, Lw.ln2w, lane);
+        row_load<D>(lv, Lw.ln2b, lane);
+      };
+      if (RPF && wave == 0) params();
       wait_for(p, C::NTP, [](int i) { return i; }, E | seq_of(l, PH_PROJ), 4);
       mark(l, PH_ROW2, 0);
       if (wave == 0) {
-        row_resid<D, C::KSP>(xr, p.p1, my_row, Lw.bproj, lane);
+        if (!RPF) params();
+        row_resid<D, C::KSP>(xr, p.p1, my_row, bv, lane);
         markv(l, PH_ROW2, 1, xr[0].x);
-        row_ln<D>(xr, Lw.ln2w, Lw.ln2b, p.eps, xn2 + (size_t)my_row * D, lane);
+        row_ln<D>(xr, gv, lv, p.eps, xn2 + (size_t)my_row * D, lane);
       }
       signal(p, E | seq_of(l, PH_ROW2));
       mark(l, PH_ROW2, 3);
@@ -988,14 +1011,21 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
     }
     // ---- x += MLP output; LN1 of the next layer (ln_f after the last) -> XN ----
     if (my_row >= 0) {
+      const bool last = l + 1 == L;
+      float4 bv[NU], gv[NU], lv[NU];
+      auto params = [&] {
+        row_load<D>(bv, Lw.bmlp, lane);
+        row_load<D>(gv, last ? p.lnfw : p.layers[l + 1].ln1w, lane);
+        row_load<D>(lv, last ? p.lnfb : p.layers[l + 1].ln1b, lane);
+      };
+      if (RPF && wave == 0) params();
       wait_for(p, C::NTM, [](int i) { return i; }, E | seq_of(l, PH_MLP), 7);
       mark(l, PH_ROW3, 0);
       if (wave == 0) {
-        row_resid<D, C::KSM>(xr, p.p1, my_row, Lw.bmlp, lane);
+        if (!RPF) params();
+        row_resid<D, C::KSM>(xr, p.p1, my_row, bv, lane);
         markv(l, PH_ROW3, 1, xr[0].x);
-        const bool last = l + 1 == L;
-        row_ln<D>(xr, last ? p.lnfw : p.layers[l + 1].ln1w, last ? p.lnfb : p.layers[l + 1].ln1b, p.eps,
-                  xn_of(2 * l + 2) + (size_t)my_row * D, lane);
+        row_ln<D>(xr, gv, lv, p.eps, xn_of(2 * l + 2) + (size_t)my_row * D, lane);
       }
       signal(p, E | seq_of(l, PH_ROW3));
       mark(l, PH_ROW3, 3);
