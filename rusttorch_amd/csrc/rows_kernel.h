@@ -924,6 +924,9 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
     if (cw && wg < C::NTF) w_dma<C::KWF>(wf, Lw.wfc, D, 4 * D, cf * TN, kwf, lane);
     // ---- c_fc (LN2 output) -> P0 ----
     if (wg < C::NTF) {
+      // mlp c_proj's weights (registers) while the row phase runs: issued
+      // after c_fc's, all 192 tiles' loads would meet c_fc's publication
+      if (wg < C::NTM && cw) w_regs<C::KWM>(wm, Lw.wmlp, 4 * D, D, cm * TN, klm, lane);
       wait_for(p, M, row_wg, E | seq_of(l, PH_ROW2), 5);
       mark(l, PH_FC, 0);
       floatx16 acc = {};  // (the poller wave passes zeros to tile_out)
@@ -947,10 +950,6 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
         if (r < M) stc(p0f + ((size_t)zf * MR + r) * (4 * D) + n0 + cc, v);
       });
       signal(p, E | seq_of(l, PH_FC));
-      // mlp c_proj's weights once the partials are published (the flag
-      // waits for every memory instruction of the wave, in whatever order
-      // loads and stores complete)
-      if (wg < C::NTM && cw) w_regs<C::KWM>(wm, Lw.wmlp, 4 * D, D, cm * TN, klm, lane);
       mark(l, PH_FC, 3);
     }
     // ---- mlp c_proj (gelu_new of the c_fc output) -> P1 ----
