@@ -532,6 +532,7 @@ struct AttLds {
   float q[TMAX * HD];
   float k[TMAX * (HD + 4)];  // padded rows: lane-per-key reads spread over the banks
   float v[TMAX * HD];
+  float mg[NCW][QG][HD + 2];  // each wave's (o, m, l) per query, merged over the waves
 };
 
 // One block of up to 64 keys [kb, kb + nk) of query t, keys from the cache
@@ -586,6 +587,54 @@ __device__ __forceinline__ void att_block(const AttLds& A, int t, int past, cons
     o += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), i)) * vv;
   }
   m = mn;
+}
+
+// Cache keys [kb, kb + nk) (all below past, so every query sees them) against
+// the nq queries t_lo .. of the item at once: lane = key for the scores, lane
+// = dim for the outputs; the block's K and V rows are read once for all the
+// queries.
+__device__ __forceinline__ void att_cache_block(const AttLds& A, int t_lo, int nq, const float* K, const float* Vg,
+                                                int kb, int nk, float (&m)[QG], float (&l)[QG], float (&o)[QG],
+                                                int lane) {
+  const bool valid = lane < nk;
+  const float* kr = K + (size_t)(kb + min(lane, nk - 1)) * HD;
+  float4 kv[HD / 4];
+#pragma unroll
+  for (int c = 0; c < HD / 4; ++c) kv[c] = ld4(kr + 4 * c);
+  float pe[QG];
+#pragma unroll
+  for (int q = 0; q < QG; ++q) {
+    pe[q] = 0.f;
+    if (q < nq) {  // wave-uniform
+      const float4* q4 = reinterpret_cast<const float4*>(A.q + (t_lo + q) * HD);
+      float dot = 0.f;
+#pragma unroll
+      for (int c = 0; c < HD / 4; ++c) {
+        const float4 qq = q4[c];
+        dot += qq.x * kv[c].x + qq.y * kv[c].y + qq.z * kv[c].z + qq.w * kv[c].w;
+      }
+      const float sc = valid ? dot * 0.125f : -__builtin_inff();  // 1 / sqrt(64)
+      const float mn = fmaxf(m[q], wmax(sc));
+      pe[q] = valid ? fexp_a(sc - mn) : 0.f;
+      const float corr = fexp_a(m[q] - mn);
+      l[q] = l[q] * corr + wsum(pe[q]);
+      o[q] *= corr;
+      m[q] = mn;
+    }
+  }
+  for (int i = 0; i < nk; i += 8) {
+    float vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) vv[u] = Vg[(size_t)(kb + min(i + u, nk - 1)) * HD + lane];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (i + u < nk) {  // wave-uniform
+#pragma unroll
+        for (int q = 0; q < QG; ++q)
+          if (q < nq) o[q] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe[q]), i + u)) * vv[u];
+      }
+    }
+  }
 }
 
 // Keys [0, k_hi) of query t in blocks of 64 (b0, b0 + bstep, ...): the cache
@@ -842,11 +891,59 @@ __global__ __launch_bounds__(NTH, 1) void rows_kernel(RParams p) {
       if (cw) att_gather<D, FRESH>(p, att, p0q, l, s, h, t_lo, t_hi, past, Kc, Vc, tid);
       __syncthreads();
       mark(l, PH_ATT, 1);
-      if (cw && t_lo + wave < t_hi) {
-        const int t = t_lo + wave;
-        float m = -__builtin_inff(), ll = 0.f, o = 0.f;
-        att_range(att, t, past, Kc, Vc, past + t + 1, 0, 1, m, ll, o, lane);
-        stc(ol + (size_t)(s * T + t) * D + h * HD + lane, o / ll);
+      if (past == 0 || D > 768) {
+        // no cached rows (or the width whose registers cannot hold the
+        // key-parallel form): wave w attends query t_lo + w over all its keys
+        if (cw && t_lo + wave < t_hi) {
+          const int t = t_lo + wave;
+          float m = -__builtin_inff(), ll = 0.f, o = 0.f;
+          att_range(att, t, past, Kc, Vc, past + t + 1, 0, 1, m, ll, o, lane);
+          stc(ol + (size_t)(s * T + t) * D + h * HD + lane, o / ll);
+        }
+      } else {
+        // cached rows: wave w takes the 64-key blocks w, w + 4, ... of the
+        // cache for all the item's queries; wave q then adds query t_lo + q's
+        // new rows; the waves' states merge in wave order
+        const int nq = t_hi - t_lo;
+        float m[QG], ll[QG], o[QG];
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+          m[q] = -__builtin_inff();
+          ll[q] = 0.f;
+          o[q] = 0.f;
+        }
+        if (cw) {
+          for (int kb = 64 * wave; kb < past; kb += 64 * NCW)
+            att_cache_block(att, t_lo, nq, Kc, Vc, kb, min(64, past - kb), m, ll, o, lane);
+#pragma unroll
+          for (int q = 0; q < QG; ++q)
+            if (q == wave && q < nq)
+              att_block<true>(att, t_lo + q, past, Kc, Vc, past, t_lo + q + 1, m[q], ll[q], o[q], lane);
+#pragma unroll
+          for (int q = 0; q < QG; ++q) {
+            att.mg[wave][q][2 + lane] = o[q];
+            if (lane == 0) {
+              att.mg[wave][q][0] = m[q];
+              att.mg[wave][q][1] = ll[q];
+            }
+          }
+        }
+        __syncthreads();
+        if (cw && wave < nq) {
+          const int q = wave;
+          float M = -__builtin_inff();
+#pragma unroll
+          for (int w = 0; w < NCW; ++w) M = fmaxf(M, att.mg[w][q][0]);
+          float L = 0.f, O = 0.f;
+#pragma unroll
+          for (int w = 0; w < NCW; ++w) {
+            const float mw = att.mg[w][q][0];
+            const float f = mw == -__builtin_inff() ? 0.f : fexp_a(mw - M);
+            L += att.mg[w][q][1] * f;
+            O += att.mg[w][q][2 + lane] * f;
+          }
+          stc(ol + (size_t)(s * T + t_lo + q) * D + h * HD + lane, O / L);
+        }
       }
       mark(l, PH_ATT, 2);
       signal(p, E | seq_of(l, PH_ATT));

@@ -6,7 +6,8 @@ kernels (RTG_NO_ROWS=1) for the greedy ids that generate_cached derives from
 the same launch (its argmax and finalize run inside it).
 
 Covered: prompts of 2..32 tokens at position 0; chunks appended behind a
-cache longer than one 64-key block (attention over cache rows and new rows);
+cache longer than one 64-key block (attention over cache rows and new rows),
+and behind up to 6 blocks (cached keys split between an item's waves);
 S sequences x T tokens with S*T = 32 on a batched cache; the two code paths
 of the kernel (n_embd 768: activations through LDS; 1024: in registers)
 and the 128-wide mini model.
@@ -58,6 +59,31 @@ def test_prompt_chunks_against_oracle(oracle_lib, name, chunks):
         worst = max(worst, check_rows(got, ref, f"{name} chunk {i} (n={n}, past={c.len() - n})"))
     assert c.len() == sum(chunks)
     print(f"[gpu] rows {name}: {sum(chunks)} rows over {len(chunks)} chunks, max |d| {worst:.3e}", flush=True)
+    c.close()
+    m.close()
+
+
+@pytest.mark.parametrize("name", ["mini", "small"])
+def test_chunks_behind_long_cache(oracle_lib, name):
+    """Chunks behind a cache of several 64-key blocks: the cached keys are
+    split between the four waves of each attention item (one to three blocks
+    each) for all of the item's queries, and the waves' softmax states are
+    merged; every chunk's rows against the oracle, the later ones at 256 and
+    more cached positions (mini holds 64 positions: one to its end)."""
+    sh = synth.SHAPES[name]
+    sd = synth.make_weights(sh)
+    m = Gpt2Model.from_state_dict(sd, cfg_of(sh))
+    om = oracle_lib.OracleModel.from_shape(sd, sh, threads=THREADS)
+    chunks = (32, 30, 2) if name == "mini" else (32,) * 8 + (31, 7, 32, 3)
+    c, oc = m.new_cache(), om.new_cache()
+    worst = 0.0
+    for i, n in enumerate(chunks):
+        ids = synth.make_tokens(n, sh.vocab_size, stream=990 + i)
+        got = m.forward_cached(ids, c)
+        ref = om.forward_cached(ids, oc)
+        if c.len() - n >= 64 or name == "mini":
+            worst = max(worst, check_rows(got, ref, f"{name} chunk {i} (n={n}, past={c.len() - n})"))
+    print(f"[gpu] rows {name}: chunks up to position {c.len()}, max |d| {worst:.3e}", flush=True)
     c.close()
     m.close()
 
