@@ -10,9 +10,11 @@
 // write partial sums; whoever consumes a GEMM's output adds them up in k
 // order:
 //   QKV    (c_attn on the LN1 output)  -> partials P0, summed + bias by ATT
-//   ATT    items (sequence, head, group of 4 queries; one query per wave):
-//          q/k/v, the group's k/v rows into the cache, causal attention
-//          over the cache and the new rows -> O
+//   ATT    items (sequence, head, group of 4 queries): q/k/v, the group's
+//          k/v rows into the cache, causal attention over the cache (its
+//          64-key blocks split between the four waves, each block scored
+//          against all the group's queries) and the new rows (one query per
+//          wave) -> O
 //   PROJ   (attn c_proj on O)          -> partials P1
 //   ROW2   one workgroup per row: x += P1 sums + bias; LN2(x) -> XN
 //   FC     (c_fc on XN)                -> partials P0
@@ -20,12 +22,16 @@
 //          is read)                    -> partials P1
 //   ROW3   x += P1 sums + bias; LN1 of the next layer (ln_f after the last)
 //          -> XN
-//   LM     tied LM head, every workgroup a strided set of 32-column tiles.
+//   LM     tied LM head, every workgroup a strided set of 32-column tiles;
+//          or, when the launch also takes the argmax for generate (at most
+//          4 sequences), a GEMV over the last row of each sequence only.
 // The residual row x stays in registers of its row workgroup for the whole
 // forward. A fifth wave per workgroup only polls, so that the compute waves
 // keep their weight prefetches (c_attn + attn c_proj at the start of a
 // layer, c_fc + mlp c_proj at the start of the MLP half) in flight while the
-// workgroup waits for its inputs.
+// workgroup waits for its inputs. Nothing that does not depend on a wait is
+// loaded after it (biases, LayerNorm rows): every load after a wait is one
+// more memory round trip on the layer's critical path.
 //
 // Synchronisation: each workgroup owns one flag (a 64-bit word on its own
 // 128-byte line) holding (epoch << 16) | sequence number of the last phase it
