@@ -284,6 +284,10 @@ hipError_t persistent_decode_step(PersistentState* s, hipStream_t stream, bool c
   // windows; both kernels keep the same decode state, so steps may alternate
   if (s->plan->tile && s->ttags && pos >= 0 && pos + 1 <= tile_max_len())
     return tile_decode_step(s->plan->tile, s->tp, stream, cooperative);
+  // test hook RTG_TEST_DECODE_WAIT="<polling rounds>": the step's layer-1
+  // input fetch times out after that many rounds (the host reports it)
+  s->p.test_spins = 0;
+  if (const char* t = getenv("RTG_TEST_DECODE_WAIT")) s->p.test_spins = (unsigned)strtoul(t, nullptr, 10);
   void* args[] = {&s->p};
   const void* fn = s->plan->kernel;
   if (cooperative) return hipLaunchCooperativeKernel(fn, dim3(pk::G), dim3(pk::NTHREADS), args, 0, stream);

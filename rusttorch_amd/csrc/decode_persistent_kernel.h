@@ -113,6 +113,10 @@ struct Params {
   unsigned* err;
   u64* trace;         // optional: per-workgroup timestamps (TRACE_STRIDE entries each)
   const void* dummy;  // >= 1 KiB of zeros: target of the loads of segments a wave does not own
+  // Test hook (test_spins > 0): layer 1's x3 fetch waits for a tag no
+  // producer writes and gives up after test_spins polling rounds, so the
+  // step takes its timeout path (error word) without a fault or hang.
+  unsigned test_spins;
 };
 
 // Optional phase trace (p.trace != null): timestamps of the 100 MHz constant
@@ -586,7 +590,7 @@ template <int RPW, int SW, int NMAX, bool SCALE = false, int D = 0>
 __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, float* dst, int gl, unsigned* err,
                                            float* dst2 = nullptr, const float* g = nullptr,
                                            const float* cen_src = nullptr, unsigned* rdy = nullptr,
-                                           unsigned rdy_n = 0, float* c0 = nullptr) {
+                                           unsigned rdy_n = 0, float* c0 = nullptr, unsigned cap = SPIN_CAP) {
   constexpr int NG = NGLUE * 64;
   constexpr int NW = (NMAX + NG - 1) / NG;
   static_assert(!SCALE || (NMAX >= D && D % 64 == 0), "a centred fetch is one polling round over D words");
@@ -618,7 +622,7 @@ __device__ __forceinline__ void glue_fetch(const u64* src, int n, unsigned tag, 
       for (int k = 0; k < NW; ++k)
         if ((unsigned)(w[k] >> 32) != tag) all = false;
       if (all) break;
-      if (++spins > SPIN_CAP || ((spins & 255u) == 0u && err_set(err))) {
+      if (++spins > cap || ((spins & 255u) == 0u && err_set(err))) {
         raise_err(err, 1u);
         break;
       }
@@ -869,9 +873,11 @@ __device__ __forceinline__ void glue_role(const Params& p, Smem<C::D>& sm, int g
         cr = PK_G(float, LP.cq)[row0 + lane];
       }
       if (l > 0) {  // centred on the mean of x2 of layer l - 1 (in LDS once all glue waves fetched it)
-        glue_fetch<GM::RPW, GM::SW, D, true, D>(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tag, sm.xraw, gl, p.err,
-                                             sm.in_vec[1], LP.ln1w, sm.x2raw[(l - 1) & 1], &sm.in_ready[PH_FC],
-                                             (unsigned)l * NGLUE, &c0q);
+        const bool tw = p.test_spins != 0u && l == 1;  // the test hook's forced timeout
+        glue_fetch<GM::RPW, GM::SW, D, true, D>(p.tag + (long)(l - 1) * p.lw + p.o_x3, D, tw ? tag + 0x5a5au : tag,
+                                             sm.xraw, gl, p.err, sm.in_vec[1], LP.ln1w, sm.x2raw[(l - 1) & 1],
+                                             &sm.in_ready[PH_FC], (unsigned)l * NGLUE, &c0q,
+                                             tw ? p.test_spins : SPIN_CAP);
         glue_input_done(sm, PH_QKV, lane);
       }
       if (leader) {

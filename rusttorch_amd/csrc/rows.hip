@@ -196,6 +196,10 @@ hipError_t rows_forward(const RowsPlan* p, RowsState* s, hipStream_t stream, flo
   a.done = head_done(s->mem);
   a.err = head_err(s->mem);
   a.trace = trace ? reinterpret_cast<rk::u64*>(trace) : trace_buf();
+  // test hook RTG_TEST_ROWS_WAIT=<wait code>: that wait times out (the
+  // host then reports the error)
+  a.force_wait = 0;
+  if (const char* t = getenv("RTG_TEST_ROWS_WAIT")) a.force_wait = (unsigned)strtoul(t, nullptr, 10);
   void* args[] = {&a};
   return hipLaunchKernel(p->kernel[s->fresh ? 1 : 0], dim3(rk::G), dim3(rk::NTH), args, 0, stream);
 }

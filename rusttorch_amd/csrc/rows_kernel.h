@@ -160,6 +160,10 @@ struct RParams {
   unsigned* done;
   unsigned* err;
   u64* trace;          // optional: [G][TRACE_WORDS] phase timestamps
+  // Test hook: the waits with code force_wait (0: none) wait for a flag
+  // value no producer writes, so they time out after their SPIN_CAP polling
+  // rounds (the error path, exercised without a fault or hang).
+  unsigned force_wait;
 };
 
 #define RK_G(T, p) ((const __attribute__((address_space(1))) T*)(p))
@@ -232,6 +236,7 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // flight meanwhile.
 template <class F>
 __device__ __forceinline__ void wait_for(const RParams& p, int n, F prod, u64 target, unsigned code) {
+  if (code == p.force_wait) target = ~0ull;
   if (wave_id() == NCW) {
     const int lane = threadIdx.x & 63;
     unsigned spins = 0;
