@@ -115,19 +115,24 @@ def test_batched_chunks_against_oracle(oracle_lib, S, T):
 def test_greedy_finish_matches_per_op_path(monkeypatch):
     """generate_cached's prefill with the argmax and finalize inside the
     multi-row launch, against the per-op prefill kernels plus the argmax and
-    finalize kernels: the same greedy ids, at batch 1 (c1's shape) and for
-    4 sequences of 8 tokens."""
+    finalize kernels: the same greedy ids, at batch 1 (c1's shape), for 4
+    sequences of 8 tokens (both with the last-row LM head) and for 8 of 4
+    (the all-rows LM head)."""
     sh = synth.SHAPES["small"]
     m = Gpt2Model.from_state_dict(synth.make_weights(sh), cfg_of(sh))
     prompt = synth.make_tokens(32, sh.vocab_size)
     prompts = synth.make_tokens(32, sh.vocab_size, stream=970).reshape(4, 8)
+    wide = synth.make_tokens(32, sh.vocab_size, stream=971).reshape(8, 4)
     a1 = m.generate_cached(prompt, 16, 0.0)
     ab = m.generate_cached_batched(prompts, 8)
+    aw = m.generate_cached_batched(wide, 8)  # 8 sequences: the all-rows LM head, keys of 8 rows
     monkeypatch.setenv("RTG_NO_ROWS", "1")
     b1 = m.generate_cached(prompt, 16, 0.0)
     bb = m.generate_cached_batched(prompts, 8)
+    bw = m.generate_cached_batched(wide, 8)
     assert a1 == b1
     assert np.array_equal(ab, bb)
+    assert np.array_equal(aw, bw)
     m.close()
 
 
