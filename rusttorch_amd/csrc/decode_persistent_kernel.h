@@ -164,6 +164,17 @@ struct Cfg {
   // the tied LM head's loads: normal for d = 768 (c1: 4.38k against 4.29k
   // tokens/s non-temporal), non-temporal otherwise (c3: 1.54k against 1.53k)
   static constexpr bool LM_NT = D_ != 768;
+  // Weights kept in the 256 MB last-level cache from step to step: loaded
+  // with normal loads, where every other layer matrix is loaded
+  // non-temporally. At d = 768 the c_attn weights (85 MB, beside wte): their
+  // refill runs during the h exchange, which then competes with less HBM
+  // traffic (c1: 205.9 against 210.6 µs per token; with the attention
+  // projections as well, 113 MB: 207.4; the first two layers instead: 209.3;
+  // wte non-temporal beside them: 209.1). At d = 1024 the attention
+  // projections (100 MB; wte is non-temporal there): c3 574.6 against 578.5
+  // µs (c_attn, 302 MB: 588.4).
+  static constexpr bool Q_NT = D_ != 768;
+  static constexpr bool P_NT = D_ != 1024;
   typedef Geom<3 * D, D, E> GQ;
   // the attention projection on the first D / 8 workgroups, 8 rows each: its
   // input then goes to (and x2 comes from) 96 workgroups at d = 768 instead
@@ -495,10 +506,10 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     lds_release();
     if (lane == 0) lds_add(&sm.gemv_done, 1);
   };
-  seg_issue<WT, MS, GQ, 0>(A, LP[0].wqkv, dz, wg, cw, lane, 0);  // needed first: no pacing
+  seg_issue<WT, MS, GQ, 0, C::Q_NT>(A, LP[0].wqkv, dz, wg, cw, lane, 0);  // needed first: no pacing
   // each refill is paced until the input of this wave's next compute is ready
   auto rdy = [&](int ph) { return &sm.in_ready[ph]; };
-  seg_issue<WT, MS, GP, C::PACE>(B, LP[0].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), NGLUE);
+  seg_issue<WT, MS, GP, C::PACE, C::P_NT>(B, LP[0].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), NGLUE);
   for (int l = 0; l + 1 < p.L; ++l) {
     const unsigned n1 = (unsigned)(l + 1) * NGLUE;
     compute_and_signal(A, sm.in_vec[1], GQ(), PH_QKV, l);   // QKV; refill A with FC
@@ -506,9 +517,9 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);  // attention projection; refill B with MLP projection
     seg_issue<WT, MS, GM, C::PACE>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
     compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);    // FC; refill A with next QKV
-    seg_issue<WT, MS, GQ, C::PACE>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
+    seg_issue<WT, MS, GQ, C::PACE, C::Q_NT>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
     compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);   // MLP projection; refill B with next attention projection
-    seg_issue<WT, MS, GP, C::PACE>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), n1 + NGLUE);
+    seg_issue<WT, MS, GP, C::PACE, C::P_NT>(B, LP[l + 1].waproj, dz, wg, cw, lane, 0, rdy(PH_QKV), n1 + NGLUE);
   }
   {  // last layer: the refills after FC / MLP projection are the LM head's chunks 0 and 1
     const int l = p.L - 1;
