@@ -161,20 +161,20 @@ struct Cfg {
   // d = 1024 (c3: 582.5 µs against 582.8 at 4, 593 at 8, 590.5 at 12, 594
   // at 2); 12 elsewhere
   static constexpr int PACE = D_ == 768 ? 8 : D_ == 1024 ? 6 : PK_PACE;
-  // the tied LM head's loads: normal for d = 768 (c1: 4.38k against 4.29k
-  // tokens/s non-temporal), non-temporal otherwise (c3: 1.54k against 1.53k)
-  static constexpr bool LM_NT = D_ != 768;
-  // Weights kept in the 256 MB last-level cache from step to step: loaded
-  // with normal loads, where every other layer matrix is loaded
-  // non-temporally. At d = 768 the c_attn weights (85 MB, beside wte): their
-  // refill runs during the h exchange, which then competes with less HBM
-  // traffic (c1: 205.9 against 210.6 µs per token; with the attention
-  // projections as well, 113 MB: 207.4; the first two layers instead: 209.3;
-  // wte non-temporal beside them: 209.1). At d = 1024 the attention
-  // projections (100 MB; wte is non-temporal there): c3 574.6 against 578.5
-  // µs (c_attn, 302 MB: 588.4).
-  static constexpr bool Q_NT = D_ != 768;
-  static constexpr bool P_NT = D_ != 1024;
+  // Cache policy of the weight loads. Matrices loaded with normal loads stay
+  // in the 256 MB last-level cache from one step to the next; the others
+  // are loaded non-temporally (~15% faster streaming, not kept). Their
+  // refills run during the exchanges (c_attn's during the h exchange, the
+  // projections' during x3 and x2), which then compete with less HBM
+  // traffic. d = 768: c_attn, attention projection and MLP projection
+  // (226 MB; wte and c_fc non-temporal): c1 202.5-202.8 µs per token; with
+  // c_fc instead of the MLP projection 202.5-202.7; c_attn alone beside a
+  // cached wte 205.6-206.5; wte alone 210.6; all four matrices (340 MB)
+  // 212.6. The multi-row forward reads the same matrices and gains too
+  // (c1 prefill 0.413-0.420 against 0.418-0.423 ms). d = 1024: the
+  // attention projections (100 MB): c3 574.6 against 578.5 µs (c_attn,
+  // 302 MB: 588.4).
+  static constexpr bool Q_NT = D_ != 768, P_NT = D_ != 768 && D_ != 1024, M_NT = D_ != 768;
   typedef Geom<3 * D, D, E> GQ;
   // the attention projection on the first D / 8 workgroups, 8 rows each: its
   // input then goes to (and x2 comes from) 96 workgroups at d = 768 instead
@@ -515,7 +515,7 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     compute_and_signal(A, sm.in_vec[1], GQ(), PH_QKV, l);   // QKV; refill A with FC
     seg_issue<WT, MS, GF, C::PACE>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
     compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);  // attention projection; refill B with MLP projection
-    seg_issue<WT, MS, GM, C::PACE>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
+    seg_issue<WT, MS, GM, C::PACE, C::M_NT>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
     compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);    // FC; refill A with next QKV
     seg_issue<WT, MS, GQ, C::PACE, C::Q_NT>(A, LP[l + 1].wqkv, dz, wg, cw, lane, 0, rdy(PH_MLP), n1);
     compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);   // MLP projection; refill B with next attention projection
@@ -527,11 +527,11 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
     compute_and_signal(A, sm.in_vec[1], GQ(), PH_QKV, l);
     seg_issue<WT, MS, GF, C::PACE>(A, LP[l].wfc, dz, wg, cw, lane, 0, rdy(PH_PROJ), n1);
     compute_and_signal(B, sm.in_vec[0], GP(), PH_PROJ, l);
-    seg_issue<WT, MS, GM, C::PACE>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
+    seg_issue<WT, MS, GM, C::PACE, C::M_NT>(B, LP[l].wmproj, dz, wg, cw, lane, 0, rdy(PH_FC), n1);
     compute_and_signal(A, sm.in_vec[1], GF(), PH_FC, l);
-    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1, p.V);
+    seg_issue<WT, MS, GL, C::PACE>(A, p.wte, dz, wg, cw, lane, 0, rdy(PH_MLP), n1, p.V);
     compute_and_signal(B, sm.in_vec[0], GM(), PH_MLP, l);
-    seg_issue<WT, MS, GL, C::PACE, C::LM_NT>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE, p.V);
+    seg_issue<WT, MS, GL, C::PACE>(B, p.wte, dz, wg, cw, lane, NC * GL::SPW, rdy(PH_LM), NGLUE, p.V);
   }
   // LM head (tied wte, gpt2.rs:392-396): chunk c = workgroup segments
   // [c*NC*SPW, (c+1)*NC*SPW), alternating between A and B.
@@ -543,9 +543,9 @@ __device__ __forceinline__ void gemv_role(const Params& p, Smem<C::D>& sm, int c
   for (int base = 0; base < segs_here; base += 2 * PER_CHUNK) {
     // nothing else is in flight now: stream at full rate
     seg_compute<WT, MS, GL>(A, sm.in_vec[1], sm.part, wg, cw, lane, base, p.V);
-    seg_issue<WT, MS, GL, 0, C::LM_NT>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK, nullptr, 0, p.V);
+    seg_issue<WT, MS, GL, 0>(A, p.wte, dz, wg, cw, lane, base + 2 * PER_CHUNK, nullptr, 0, p.V);
     seg_compute<WT, MS, GL>(B, sm.in_vec[1], sm.part, wg, cw, lane, base + PER_CHUNK, p.V);
-    seg_issue<WT, MS, GL, 0, C::LM_NT>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK, nullptr, 0, p.V);
+    seg_issue<WT, MS, GL, 0>(B, p.wte, dz, wg, cw, lane, base + 3 * PER_CHUNK, nullptr, 0, p.V);
   }
   lds_release();
   if (lane == 0) lds_add(&sm.gemv_done, 1);
