@@ -156,11 +156,12 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 template <int D_, int V_, int WT_>
 struct Cfg {
   static constexpr int D = D_, V = V_, WT = WT_, H = D_ / HD, E = WT_ == W_BF16 ? 8 : 4;
-  // refill pacing (seg_issue): measured best at 8 for d = 768 (c1: 210.3 µs
-  // per token against 209.9 at 6, 211.5 at 4, 218.8 at 12) and at 6 for
+  // refill pacing (seg_issue): measured best at 4 for d = 768 with the
+  // cache policy below (c1: 203.2-203.8 µs per token against 203.6-203.9 at
+  // 2, 204.1-204.7 at 8, 209.9 at 12, 211.3 without pacing) and at 6 for
   // d = 1024 (c3: 582.5 µs against 582.8 at 4, 593 at 8, 590.5 at 12, 594
   // at 2); 12 elsewhere
-  static constexpr int PACE = D_ == 768 ? 8 : D_ == 1024 ? 6 : PK_PACE;
+  static constexpr int PACE = D_ == 768 ? 4 : D_ == 1024 ? 6 : PK_PACE;
   // Cache policy of the weight loads. Matrices loaded with normal loads stay
   // in the 256 MB last-level cache from one step to the next; the others
   // are loaded non-temporally (~15% faster streaming, not kept). Their
